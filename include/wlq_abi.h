@@ -1,0 +1,132 @@
+/*
+ * wlq_abi.h -- C ABI of the MI355X (gfx950) WLQ metalog-LUT quantized linear layer.
+ *
+ * Library: qwen_wlqfastshot_helen_beta_amd/libwlq_hip.so
+ *
+ * Every entry point takes plain pointers and sizes (no framework types).  fp16
+ * buffers are IEEE binary16 passed as void*.  Device entry points are
+ * asynchronous on `stream` and never synchronize; host entry points run on
+ * the calling CPU thread.  All return an int status (WLQ_OK on success); the
+ * message of the last failure on the calling thread is wlq_last_error().
+ *
+ * Data layouts (identical to the reference's, vllm_wlq/linear_method.py:284-338):
+ *   q_packed      int32 [N * wpr], code (n,k) at word n*wpr + k/spw, bit (k%spw)*bits,
+ *                 spw = 10 for 3-bit else 32/bits, wpr = words_per_row(K, bits)
+ *   lut_c         fp16 [N, 2^bits] (group_size 0) or [N, ceil(K/G), 2^bits] (group_size G)
+ *   chunk_offsets int32 [N, nch+1], chunk_cols uint16 [nnz], chunk_vals uint8 [nnz] (e5m2),
+ *                 chunk width 512 (640 for 3-bit), nch = ceil(K / chunk width)
+ *   DoRA          lora_B fp16 [N, r], lora_h / lora_H fp32 [M, r], dora_gamma fp16 [N]
+ *
+ * Optional operands: the outlier correction runs only when chunk_offsets,
+ * chunk_cols and chunk_vals are all non-null; the DoRA epilogue only when
+ * lora_B, lora_h/lora_H and dora_gamma are non-null and r > 0 (as in the
+ * reference, csrc/gemv_kernel.cu:440, csrc/gemm_kernel.cu:557).
+ *
+ * group_size: 0 = one LUT per output row (the reference).  Otherwise a
+ * multiple of 32 columns, at least the code window (32/40/64/128 columns for
+ * 4/3/2/1 bits) and below 4096; a group_size >= K is the per-row case.
+ *
+ * Workspace: split-K partial sums (fp32).  Pass the buffer and its size; when
+ * it is smaller than wlq_gemm_workspace_bytes() the split count is reduced to
+ * what fits (no workspace at all is always valid).  Calls that share one
+ * workspace must be ordered on one stream.
+ */
+#ifndef WLQ_ABI_H
+#define WLQ_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WLQ_ABI_VERSION 1
+
+enum wlq_status {
+  WLQ_OK = 0,
+  WLQ_ERR_NULL_POINTER = 1, /* a required pointer is null */
+  WLQ_ERR_BAD_SHAPE = 2,    /* negative/oversized size or inconsistent words_per_row */
+  WLQ_ERR_UNSUPPORTED = 3,  /* bits or group_size outside the supported set */
+  WLQ_ERR_CAPACITY = 4,     /* an output buffer is too small */
+  WLQ_ERR_HIP = 5,          /* the HIP runtime reported an error */
+  WLQ_ERR_FORMAT = 6        /* malformed input stream */
+};
+
+int wlq_abi_version(void);
+const char* wlq_status_string(int status);
+const char* wlq_last_error(void);
+
+/* Words per packed row: 4 * ceil(ceil(K / spw) / 4).
+ * Reference: vllm_wlq/linear_method.py:329-330, csrc/vllm_binding.cpp:209-210. */
+int64_t wlq_words_per_row(int64_t K, int32_t bits);
+
+/* Outlier chunk width: 640 for 3-bit, else 512. Reference: csrc/vllm_binding.cpp:279,351. */
+int32_t wlq_chunk_width(int32_t bits);
+
+/* Workspace bytes the split-K plan of wlq_gemm (M rows) would like on `device`
+ * (0 when no split is planned).  wlq_gemv uses M = 1. */
+size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, int32_t device);
+
+/* Decode product, one activation row: out[N] = fp16((x . W0^T + s * lora_h . lora_B^T) * gamma).
+ * Replaces launch_gemv_chunk_csr (csrc/gemv_kernel.cu:396-457; declared at
+ * csrc/vllm_binding.cpp:10-29), whose caller passes M(=K) and num_chunks and a
+ * workspace it owns; here num_chunks is derived from K and bits. */
+int wlq_gemv(const int32_t* q_packed, const void* lut_c, const void* x, void* out,
+             const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals,
+             const void* lora_B, const float* lora_h, const void* dora_gamma, float lora_scale, int32_t r,
+             int64_t N, int64_t K, int32_t bits, int32_t group_size,
+             void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Product for M activation rows: out[M, N] = fp16((X . W0^T + s * lora_H . lora_B^T) * gamma).
+ * Replaces both branches of gemm_forward (csrc/vllm_binding.cpp:318-419): the
+ * fused small-M kernel launch_gemm_metalog_dora (csrc/gemm_kernel.cu:527-596,
+ * declared csrc/vllm_binding.cpp:31-52) and the M >= 16 sequence
+ * dequant -> at::mm_out -> launch_fused_dora_epilogue.  M <= 32 runs the
+ * weight-streaming MFMA kernel, larger M the LDS-staged MFMA GEMM.
+ * words_per_row must equal wlq_words_per_row(K, bits). */
+int wlq_gemm(const void* X, const int32_t* q_packed, const void* lut_c, void* out,
+             int64_t M, int64_t N, int64_t K, int32_t bits, int64_t words_per_row, int32_t group_size,
+             const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals,
+             const float* lora_H, const void* lora_B, const void* dora_gamma, float lora_scale, int32_t r,
+             void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Bit-exact W_out[N, K] (fp16) = lut[n, g(k), code(n, k)], outliers overwritten with e5m2 << 8.
+ * Replaces launch_dequant_patch_metalog (csrc/gemm_kernel.cu:475-503, declared
+ * csrc/vllm_binding.cpp:54-68). */
+int wlq_dequant(const int32_t* q_packed, const void* lut_c, void* W_out, int64_t N, int64_t K, int32_t bits,
+                int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets,
+                const uint16_t* chunk_cols, const uint8_t* chunk_vals, hipStream_t stream);
+
+/* In place: out[M, N] = fp16((out + s * lora_H . lora_B^T) * gamma).
+ * Replaces launch_fused_dora_epilogue (csrc/gemm_kernel.cu:505-525, declared
+ * csrc/vllm_binding.cpp:70-80). */
+int wlq_dora_epilogue(void* out, const float* lora_H, const void* lora_B, const void* dora_gamma,
+                      float lora_scale, int32_t r, int64_t M, int64_t N, hipStream_t stream);
+
+/* Host: continuous (on-disk) packing -> row-aligned packing; symbols past the
+ * end of src read as 0.  dst must hold N * wlq_words_per_row(K, bits) words.
+ * Replaces repack_q_indices_row_aligned_cpp (csrc/vllm_binding.cpp:198-236). */
+int wlq_repack_row_aligned(const uint32_t* src, int64_t src_words, int64_t N, int64_t K, int32_t bits,
+                           uint32_t* dst, int64_t dst_words);
+
+/* Host: number of outliers an Elias-Fano tile stream declares (sum of m over
+ * tiles), an upper bound for wlq_ef_decode_chunk_csr's cols capacity. */
+int64_t wlq_ef_total(const int64_t* tile_meta, int64_t num_tiles);
+
+/* Host: Elias-Fano tile stream -> chunk CSR (offsets [N, nch+1], cols).
+ * tile_meta int64 [num_tiles, 2] = (start_bit, m), tiles row-major over the
+ * K-padded grid of tile_size x tile_size cells.  Coordinates outside
+ * [0,N) x [0,K) are dropped; *nnz_out receives the number written to cols.
+ * Replaces decode_ef_to_chunk_csr_cpp (csrc/vllm_binding.cpp:94-196). */
+int wlq_ef_decode_chunk_csr(const int64_t* tile_meta, int64_t num_tiles, const uint32_t* bitstream,
+                            int64_t stream_words, int64_t N, int64_t K, int64_t tile_size, int64_t chunk_m,
+                            int32_t* offsets, uint16_t* cols, int64_t cols_capacity, int64_t* nnz_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WLQ_ABI_H */

@@ -1,0 +1,229 @@
+// extern "C" device entry points of libwlq_hip.so (declared in include/wlq_abi.h):
+// argument validation, per-device launch planning and kernel dispatch.
+//
+// Unlike the reference launchers (csrc/gemv_kernel.cu:442-456 has no default
+// case for unsupported widths; csrc/gemm_kernel.cu:573-575 only printf's), every
+// invalid argument returns a status before anything is launched.  The CU count
+// used for split planning is cached per device (the reference caches the first
+// device's value for all devices, csrc/gemv_kernel.cu:355-363).
+#include <atomic>
+
+#include "wlq_abi.h"
+#include "wlq_internal.h"
+
+namespace wlq {
+void set_error(const char* fmt, ...);
+int window_cols_for(int bits);
+}  // namespace wlq
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cu_count[kMaxDevices];
+
+int cu_count_for(int device) {
+  if (device < 0 || device >= kMaxDevices) return 256;
+  int v = g_cu_count[device].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    cus = 256;
+  }
+  g_cu_count[device].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+int current_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    dev = 0;
+  }
+  return cu_count_for(dev);
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return WLQ_OK;
+  wlq::set_error("%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+  return WLQ_ERR_HIP;
+}
+
+// Shared shape/format validation; fills the kernel-side layer description.
+int make_layer(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K, int32_t bits, int64_t wpr_given,
+               int32_t group_size, const int32_t* offs, const uint16_t* cols, const uint8_t* vals, const char* fn,
+               wlq::Layer* L) {
+  if (bits < 1 || bits > 4) {
+    wlq::set_error("%s: unsupported bits=%d (supported: 1, 2, 3, 4)", fn, (int)bits);
+    return WLQ_ERR_UNSUPPORTED;
+  }
+  if (N < 0 || K < 0 || N > 0x3fffffff || K > 0x3fffffff) {
+    wlq::set_error("%s: bad shape N=%lld K=%lld", fn, (long long)N, (long long)K);
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  const int64_t wpr = wlq_words_per_row(K, bits);
+  if (wpr_given >= 0 && wpr_given != wpr) {
+    wlq::set_error("%s: words_per_row=%lld does not match K=%lld, bits=%d (expected %lld)", fn,
+                   (long long)wpr_given, (long long)K, (int)bits, (long long)wpr);
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  if (N * wpr > ((int64_t)1 << 40)) {
+    wlq::set_error("%s: packed weight too large", fn);
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  int ng = 1;
+  int gs = group_size;
+  if (gs < 0) {
+    wlq::set_error("%s: group_size must be >= 0, got %d", fn, (int)gs);
+    return WLQ_ERR_UNSUPPORTED;
+  }
+  if (gs > 0 && gs >= K) gs = 0;  // a single group is the per-row layout
+  if (gs > 0) {
+    const int win = wlq::window_cols_for(bits);
+    if (gs % 32 != 0 || gs < win || gs >= 4096 || K >= (1 << 20)) {
+      wlq::set_error("%s: unsupported group_size=%d for bits=%d, K=%lld (need a multiple of 32, >= %d, < 4096, "
+                     "and K < 2^20)",
+                     fn, (int)group_size, (int)bits, (long long)K, win);
+      return WLQ_ERR_UNSUPPORTED;
+    }
+    ng = (int)((K + gs - 1) / gs);
+  }
+  if (N > 0 && (lut_c == nullptr || (wpr > 0 && q_packed == nullptr))) {
+    wlq::set_error("%s: q_packed and lut_c must be non-null", fn);
+    return WLQ_ERR_NULL_POINTER;
+  }
+  // 16-byte code/LUT loads need aligned bases (row strides keep the alignment).
+  if ((reinterpret_cast<uintptr_t>(q_packed) & 15u) != 0 || (reinterpret_cast<uintptr_t>(lut_c) & 15u) != 0) {
+    wlq::set_error("%s: q_packed and lut_c must be 16-byte aligned", fn);
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  const bool csr = offs != nullptr && cols != nullptr && vals != nullptr;
+  L->q = reinterpret_cast<const uint32_t*>(q_packed);
+  L->lut = reinterpret_cast<const uint16_t*>(lut_c);
+  L->offsets = csr ? offs : nullptr;
+  L->cols = csr ? cols : nullptr;
+  L->vals = csr ? vals : nullptr;
+  L->N = (int)N;
+  L->K = (int)K;
+  L->bits = bits;
+  L->wpr = (int)wpr;
+  L->group_size = gs;
+  L->ng = ng;
+  L->chunk = wlq_chunk_width(bits);
+  L->nch = (int)((K + L->chunk - 1) / L->chunk);
+  return WLQ_OK;
+}
+
+wlq::Dora make_dora(const void* lora_B, const float* lora_H, const void* dora_gamma, float scale, int32_t r) {
+  wlq::Dora D{};
+  if (lora_B != nullptr && lora_H != nullptr && dora_gamma != nullptr && r > 0) {
+    D.B = reinterpret_cast<const uint16_t*>(lora_B);
+    D.H = lora_H;
+    D.gamma = reinterpret_cast<const uint16_t*>(dora_gamma);
+    D.scale = scale;
+    D.r = r;
+  }
+  return D;
+}
+
+int run_product(const wlq::Layer& L, const wlq::Dora& D, const void* X, void* out, int64_t M, void* workspace,
+                size_t workspace_bytes, hipStream_t stream, const char* fn) {
+  if (M < 0 || M > 0x7fffffff / 4) {
+    wlq::set_error("%s: bad M=%lld", fn, (long long)M);
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  if (M == 0 || L.N == 0) return WLQ_OK;
+  if (X == nullptr || out == nullptr) {
+    wlq::set_error("%s: activation and output pointers must be non-null", fn);
+    return WLQ_ERR_NULL_POINTER;
+  }
+  const int cus = current_cu_count();
+  size_t ws = workspace != nullptr ? workspace_bytes : 0;
+  const uint16_t* x = reinterpret_cast<const uint16_t*>(X);
+  uint16_t* y = reinterpret_cast<uint16_t*>(out);
+  float* w = reinterpret_cast<float*>(workspace);
+  if (M <= wlq::skinny_max_m()) {
+    const wlq::SplitPlan p = wlq::plan_skinny(L, (int)M, cus, ws);
+    return hip_status(wlq::launch_skinny(L, D, x, y, (int)M, p, w, stream), fn);
+  }
+  const wlq::SplitPlan p = wlq::plan_gemm(L, (int)M, cus, ws);
+  return hip_status(wlq::launch_gemm(L, D, x, y, (int)M, p, w, stream), fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, int32_t device) {
+  if (bits < 1 || bits > 4 || M <= 0 || N <= 0 || K < 0) return 0;
+  wlq::Layer L{};
+  L.N = (int)N;
+  L.K = (int)K;
+  L.bits = bits;
+  L.wpr = (int)wlq_words_per_row(K, bits);
+  L.chunk = wlq_chunk_width(bits);
+  L.nch = (int)((K + L.chunk - 1) / L.chunk);
+  const int cus = device >= 0 ? cu_count_for(device) : current_cu_count();
+  const size_t unlimited = ~(size_t)0;
+  const wlq::SplitPlan p = (M <= wlq::skinny_max_m()) ? wlq::plan_skinny(L, (int)M, cus, unlimited)
+                                                       : wlq::plan_gemm(L, (int)M, cus, unlimited);
+  return p.workspace_bytes;
+}
+
+int wlq_gemv(const int32_t* q_packed, const void* lut_c, const void* x, void* out, const int32_t* chunk_offsets,
+             const uint16_t* chunk_cols, const uint8_t* chunk_vals, const void* lora_B, const float* lora_h,
+             const void* dora_gamma, float lora_scale, int32_t r, int64_t N, int64_t K, int32_t bits,
+             int32_t group_size, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  wlq::Layer L{};
+  int st = make_layer(q_packed, lut_c, N, K, bits, -1, group_size, chunk_offsets, chunk_cols, chunk_vals,
+                      "wlq_gemv", &L);
+  if (st != WLQ_OK) return st;
+  const wlq::Dora D = make_dora(lora_B, lora_h, dora_gamma, lora_scale, r);
+  return run_product(L, D, x, out, 1, workspace, workspace_bytes, stream, "wlq_gemv");
+}
+
+int wlq_gemm(const void* X, const int32_t* q_packed, const void* lut_c, void* out, int64_t M, int64_t N, int64_t K,
+             int32_t bits, int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets,
+             const uint16_t* chunk_cols, const uint8_t* chunk_vals, const float* lora_H, const void* lora_B,
+             const void* dora_gamma, float lora_scale, int32_t r, void* workspace, size_t workspace_bytes,
+             hipStream_t stream) {
+  wlq::Layer L{};
+  int st = make_layer(q_packed, lut_c, N, K, bits, words_per_row, group_size, chunk_offsets, chunk_cols, chunk_vals,
+                      "wlq_gemm", &L);
+  if (st != WLQ_OK) return st;
+  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_scale, r);
+  return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, "wlq_gemm");
+}
+
+int wlq_dequant(const int32_t* q_packed, const void* lut_c, void* W_out, int64_t N, int64_t K, int32_t bits,
+                int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets, const uint16_t* chunk_cols,
+                const uint8_t* chunk_vals, hipStream_t stream) {
+  wlq::Layer L{};
+  int st = make_layer(q_packed, lut_c, N, K, bits, words_per_row, group_size, chunk_offsets, chunk_cols, chunk_vals,
+                      "wlq_dequant", &L);
+  if (st != WLQ_OK) return st;
+  if (N == 0 || K == 0) return WLQ_OK;
+  if (W_out == nullptr) {
+    wlq::set_error("wlq_dequant: W_out must be non-null");
+    return WLQ_ERR_NULL_POINTER;
+  }
+  return hip_status(wlq::launch_dequant(L, reinterpret_cast<uint16_t*>(W_out), stream), "wlq_dequant");
+}
+
+int wlq_dora_epilogue(void* out, const float* lora_H, const void* lora_B, const void* dora_gamma, float lora_scale,
+                      int32_t r, int64_t M, int64_t N, hipStream_t stream) {
+  if (M < 0 || N < 0 || M > 0x7fffffff || N > 0x7fffffff) {
+    wlq::set_error("wlq_dora_epilogue: bad shape M=%lld N=%lld", (long long)M, (long long)N);
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_scale, r);
+  if (M == 0 || N == 0 || D.r == 0) return WLQ_OK;
+  if (out == nullptr) {
+    wlq::set_error("wlq_dora_epilogue: out must be non-null");
+    return WLQ_ERR_NULL_POINTER;
+  }
+  return hip_status(wlq::launch_dora_epilogue(reinterpret_cast<uint16_t*>(out), (int)M, (int)N, D, stream),
+                    "wlq_dora_epilogue");
+}
+
+}  // extern "C"

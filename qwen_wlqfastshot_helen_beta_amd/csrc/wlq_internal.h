@@ -1,0 +1,58 @@
+// Internal (C++) launch interface between the C ABI layer and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace wlq {
+
+// One quantized layer as the kernels see it (all device pointers).
+struct Layer {
+  const uint32_t* q;        // [N * wpr] row-aligned codes
+  const uint16_t* lut;      // fp16 bits [N, ng, 2^bits]
+  const int32_t* offsets;   // [N, nch + 1] or nullptr (no outliers)
+  const uint16_t* cols;     // [nnz]
+  const uint8_t* vals;      // [nnz] e5m2 bytes
+  int N, K, bits, wpr;
+  int group_size;           // 0: one LUT per row
+  int ng;                   // LUT groups per row
+  int nch, chunk;           // outlier chunks per row and chunk width
+};
+
+// DoRA epilogue operands: y = (acc + scale * H[i,:] . B[n,:]) * gamma[n].
+struct Dora {
+  const uint16_t* B;        // fp16 [N, r]
+  const float* H;           // fp32 [M, r]
+  const uint16_t* gamma;    // fp16 [N]
+  float scale;
+  int r;                    // 0 disables the epilogue
+};
+
+struct SplitPlan {
+  int splits;               // blocks along K
+  int slabs_per_split;      // K range per block, in slabs
+  int seg_slabs;            // activation staging segment, in slabs
+  size_t workspace_bytes;   // fp32 partials needed (0 when splits == 1)
+};
+
+int slab_cols(int bits);             // columns one 16-row wave tile covers per step
+int skinny_max_m();
+SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_bytes);
+hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint16_t* out, int M,
+                         const SplitPlan& plan, float* workspace, hipStream_t stream);
+
+SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes);
+hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_t* out, int M,
+                       const SplitPlan& plan, float* workspace, hipStream_t stream);
+
+hipError_t launch_dequant(const Layer& L, uint16_t* W, hipStream_t stream);
+
+// Sum of fp32 split-K partials [splits, M, N] followed by the DoRA epilogue.
+hipError_t launch_splitk_reduce(const float* partial, int splits, int M, int N, const Dora& D, uint16_t* out,
+                                hipStream_t stream);
+
+// In-place epilogue on an fp16 output (the reference's separate pass).
+hipError_t launch_dora_epilogue(uint16_t* out, int M, int N, const Dora& D, hipStream_t stream);
+
+}  // namespace wlq
