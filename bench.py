@@ -4,11 +4,13 @@
 Headline: the seven Qwen2.5-7B decoder-layer
 projections (q, k, v, o, gate, up, down) at M = 1 activation row, 4-bit codes,
 fp16 LUTs per group of 128 columns, DoRA rank 16, 0.5% CSR outliers.  A step
-is one pass of ``WLQLinearMethod.apply`` over the seven projections (what
-vLLM calls per decode step), captured in a HIP graph as vLLM's decode loop
+is one decoder layer's linear work as vLLM issues it: ``WLQLinearMethod.apply``
+on the four linear layers qkv_proj (q|k|v merged), o_proj, gate_up_proj
+(gate|up merged) and down_proj, captured in a HIP graph as vLLM's decode loop
 is; steps rotate over several copies of the weights (>= 512 MB in total) so
 HBM, not the 256 MB Infinity Cache, serves them.  ``value`` = code + LUT +
-outlier bytes per step / step time (GB/s).
+outlier bytes per step / step time (GB/s); the bytes are those of the seven
+projections.
 
 Also reported: the dominant kernel's roofline (the gate_proj decode product,
 timed with HIP events on its stream), the per-shape M = 1 rates, the M = 2048
@@ -102,20 +104,27 @@ def main() -> int:
     layers = {n: synth.make_layer(*synth.QWEN25_7B_SHAPES[n], bits=4, group_size=128, rank=16, density=0.005,
                                   seed=i) for i, n in enumerate(names)}
     log(f"[bench] synthetic layers built in {time.time() - t0:.1f}s")
+    merged = {"qkv_proj": synth.merge_layers([layers["q_proj"], layers["k_proj"], layers["v_proj"]]),
+              "o_proj": layers["o_proj"],
+              "gate_up_proj": synth.merge_layers([layers["gate_proj"], layers["up_proj"]]),
+              "down_proj": layers["down_proj"]}
     step_bytes = sum(L.headline_bytes() for L in layers.values())
-    aux_bytes = sum(L.aux_bytes(1) for L in layers.values())
+    assert step_bytes == sum(L.headline_bytes() for L in merged.values())
+    aux_bytes = sum(L.aux_bytes(1) for L in merged.values())
     copies = max(2, math.ceil(512e6 / step_bytes) + 1)
     method = WLQLinearMethod(vw.WLQFastShotConfig(bits=4, group_size=128))
+    vnames = list(merged)
     mods = [{n: attach_synthetic(torch.nn.Module(), layers[n], dev) for n in names} for _ in range(copies)]
+    vmods = [{n: attach_synthetic(torch.nn.Module(), merged[n], dev) for n in vnames} for _ in range(copies)]
     vw.init_workspaces(max(L.N for L in layers.values()), max(L.K for L in layers.values()), dev)
     xs = {K: torch.randn(1, K, device=dev).half() for K in {L.K for L in layers.values()}}
     log(f"[bench] {copies} weight copies, {copies * step_bytes / 1e6:.0f} MB resident")
 
-    # ---- headline: the decoder layer's seven projections, one graph per weight copy
+    # ---- headline: the decoder layer's four vLLM linear calls, one graph per weight copy
     def layer_step(c):
         def fn():
-            for n in names:
-                method.apply(mods[c][n], xs[mods[c][n].K])
+            for n in vnames:
+                method.apply(vmods[c][n], xs[vmods[c][n].K])
         return fn
 
     graphs = [graph_of(layer_step(c)) for c in range(copies)]
@@ -133,20 +142,18 @@ def main() -> int:
         L = layers[n]
         xm = torch.randn(M, L.K, device=dev).half()
         outs = [torch.empty(M, L.N, device=dev, dtype=torch.float16) for _ in range(copies)]
-        Hs = torch.nn.functional.linear(xm, mods[0][n].lora_A_f16).float()
-
         def fn_for(c):
             m = mods[c][n]
 
-            def fn():
+            def fn():  # the op with lora_A: DoRA H computed inside the product
                 if M == 1:
                     torch.ops.wlq_fastShot.gemv(m.q_packed_aligned, m.lut_c, xm[0], outs[c][0], L.N, L.K, 4,
-                                                m.chunk_offsets, m.chunk_cols, m.chunk_vals, m.lora_B, Hs[0],
-                                                m.dora_gamma, 1.0, 128)
+                                                m.chunk_offsets, m.chunk_cols, m.chunk_vals, m.lora_B, None,
+                                                m.dora_gamma, 1.0, 128, m.lora_A_f16)
                 else:
                     torch.ops.wlq_fastShot.gemm(xm, m.q_packed_aligned, m.lut_c, outs[c], L.N, L.K, 4, L.wpr,
-                                                m.chunk_offsets, m.chunk_cols, m.chunk_vals, Hs, m.lora_B,
-                                                m.dora_gamma, 1.0, 128)
+                                                m.chunk_offsets, m.chunk_cols, m.chunk_vals, None, m.lora_B,
+                                                m.dora_gamma, 1.0, 128, m.lora_A_f16)
             return fn
 
         return [graph_of(fn_for(c)) for c in range(copies)]
@@ -217,8 +224,9 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic (seeded metalog LUTs, uniform 4-bit codes, random DoRA/outliers)",
-        "config": {"workload": "cfg1: Qwen2.5-7B decoder-layer projections q,k,v,o,gate,up,down at M=1; 4-bit, "
-                               "LUT group 128, DoRA r=16, 0.5% CSR outliers; HIP-graph step over weight copies",
+        "config": {"workload": "cfg1: Qwen2.5-7B decoder layer at M=1 (q,k,v,o,gate,up,down issued as vLLM's "
+                               "qkv/o/gate_up/down linears); 4-bit, LUT group 128, DoRA r=16, 0.5% CSR outliers; "
+                               "HIP-graph step over weight copies",
                    "M": 1, "bits": 4, "group_size": 128, "rank": 16, "outlier_density": 0.005,
                    "bytes_per_step": step_bytes, "aux_bytes_per_step": aux_bytes, "weight_copies": copies},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),

@@ -19,17 +19,24 @@
  *
  * Optional operands: the outlier correction runs only when chunk_offsets,
  * chunk_cols and chunk_vals are all non-null; the DoRA epilogue only when
- * lora_B, lora_h/lora_H and dora_gamma are non-null and r > 0 (as in the
- * reference, csrc/gemv_kernel.cu:440, csrc/gemm_kernel.cu:557).
+ * lora_B and dora_gamma are non-null, r > 0 and H is available (as in the
+ * reference, csrc/gemv_kernel.cu:440, csrc/gemm_kernel.cu:557).  H is either
+ * passed (lora_h / lora_H, fp32) or, when that pointer is null and lora_A
+ * (fp16 [r, K]) is given, computed here as fp32(fp16(x . lora_A^T)) -- the
+ * reference caller's F.linear in fp16 followed by .float()
+ * (vllm_wlq/linear_method.py:963,984) -- fused into the decode kernel for
+ * M <= 32 and r <= 64.
  *
  * group_size: 0 = one LUT per output row (the reference).  Otherwise a
  * multiple of 32 columns, at least the code window (32/40/64/128 columns for
  * 4/3/2/1 bits) and below 4096; a group_size >= K is the per-row case.
  *
- * Workspace: split-K partial sums (fp32).  Pass the buffer and its size; when
- * it is smaller than wlq_gemm_workspace_bytes() the split count is reduced to
- * what fits (no workspace at all is always valid).  Calls that share one
- * workspace must be ordered on one stream.
+ * Workspace: split-K partial sums (fp32) and, when H is computed from
+ * lora_A, its partial sums.  Pass the buffer and its size; when it is smaller
+ * than wlq_gemm_workspace_bytes() the split count is reduced to what fits.  No
+ * workspace is valid unless H has to be computed from lora_A (then
+ * WLQ_ERR_CAPACITY reports the minimum).  Calls that share one workspace must
+ * be ordered on one stream.
  */
 #ifndef WLQ_ABI_H
 #define WLQ_ABI_H
@@ -43,7 +50,7 @@
 extern "C" {
 #endif
 
-#define WLQ_ABI_VERSION 1
+#define WLQ_ABI_VERSION 2
 
 enum wlq_status {
   WLQ_OK = 0,
@@ -66,9 +73,9 @@ int64_t wlq_words_per_row(int64_t K, int32_t bits);
 /* Outlier chunk width: 640 for 3-bit, else 512. Reference: csrc/vllm_binding.cpp:279,351. */
 int32_t wlq_chunk_width(int32_t bits);
 
-/* Workspace bytes the split-K plan of wlq_gemm (M rows) would like on `device`
- * (0 when no split is planned).  wlq_gemv uses M = 1. */
-size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, int32_t device);
+/* Workspace bytes wlq_gemm (M rows) would like on `device` for DoRA rank r
+ * (r = 0: no DoRA, or H passed by the caller).  wlq_gemv uses M = 1. */
+size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, int32_t r, int32_t device);
 
 /* Decode product, one activation row: out[N] = fp16((x . W0^T + s * lora_h . lora_B^T) * gamma).
  * Replaces launch_gemv_chunk_csr (csrc/gemv_kernel.cu:396-457; declared at
@@ -76,8 +83,8 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
  * workspace it owns; here num_chunks is derived from K and bits. */
 int wlq_gemv(const int32_t* q_packed, const void* lut_c, const void* x, void* out,
              const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals,
-             const void* lora_B, const float* lora_h, const void* dora_gamma, float lora_scale, int32_t r,
-             int64_t N, int64_t K, int32_t bits, int32_t group_size,
+             const void* lora_B, const float* lora_h, const void* dora_gamma, const void* lora_A,
+             float lora_scale, int32_t r, int64_t N, int64_t K, int32_t bits, int32_t group_size,
              void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Product for M activation rows: out[M, N] = fp16((X . W0^T + s * lora_H . lora_B^T) * gamma).
@@ -90,8 +97,8 @@ int wlq_gemv(const int32_t* q_packed, const void* lut_c, const void* x, void* ou
 int wlq_gemm(const void* X, const int32_t* q_packed, const void* lut_c, void* out,
              int64_t M, int64_t N, int64_t K, int32_t bits, int64_t words_per_row, int32_t group_size,
              const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals,
-             const float* lora_H, const void* lora_B, const void* dora_gamma, float lora_scale, int32_t r,
-             void* workspace, size_t workspace_bytes, hipStream_t stream);
+             const float* lora_H, const void* lora_B, const void* dora_gamma, const void* lora_A,
+             float lora_scale, int32_t r, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Bit-exact W_out[N, K] (fp16) = lut[n, g(k), code(n, k)], outliers overwritten with e5m2 << 8.
  * Replaces launch_dequant_patch_metalog (csrc/gemm_kernel.cu:475-503, declared

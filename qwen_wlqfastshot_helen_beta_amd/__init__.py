@@ -46,11 +46,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         "wlq_last_error": (ctypes.c_char_p, []),
         "wlq_words_per_row": (c_i64, [c_i64, c_i32]),
         "wlq_chunk_width": (c_i32, [c_i32]),
-        "wlq_gemm_workspace_bytes": (c_sz, [c_i64, c_i64, c_i64, c_i32, c_i32]),
-        "wlq_gemv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, c_f, c_i32, c_i64, c_i64, c_i32, c_i32,
-                                    vp, c_sz, vp]),
+        "wlq_gemm_workspace_bytes": (c_sz, [c_i64, c_i64, c_i64, c_i32, c_i32, c_i32]),
+        "wlq_gemv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, c_f, c_i32, c_i64, c_i64, c_i32,
+                                    c_i32, vp, c_sz, vp]),
         "wlq_gemm": (ctypes.c_int, [vp, vp, vp, vp, c_i64, c_i64, c_i64, c_i32, c_i64, c_i32, vp, vp, vp, vp, vp, vp,
-                                    c_f, c_i32, vp, c_sz, vp]),
+                                    vp, c_f, c_i32, vp, c_sz, vp]),
         "wlq_dequant": (ctypes.c_int, [vp, vp, vp, c_i64, c_i64, c_i32, c_i64, c_i32, vp, vp, vp, vp]),
         "wlq_dora_epilogue": (ctypes.c_int, [vp, vp, vp, vp, c_f, c_i32, c_i64, c_i64, vp]),
         "wlq_repack_row_aligned": (ctypes.c_int, [vp, c_i64, c_i64, c_i64, c_i32, vp, c_i64]),

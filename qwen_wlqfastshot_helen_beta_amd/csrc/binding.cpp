@@ -4,7 +4,8 @@
 // binding (csrc/vllm_binding.cpp:455-532): gemv_forward, gemm_forward,
 // dequant_w0, init_workspaces, decode_ef_to_chunk_csr,
 // repack_q_indices_row_aligned.  Extensions are trailing defaulted arguments
-// only (group_size).  Every device call goes through the C ABI of
+// only: group_size (LUT per group of columns) and lora_A (compute the DoRA H
+// inside the product instead of taking lora_h / lora_H).  Every device call goes through the C ABI of
 // libwlq_hip.so (include/wlq_abi.h) on torch's current HIP stream.
 //
 // Differences from the reference, all stricter: dtypes, devices, contiguity and
@@ -91,10 +92,12 @@ void init_workspaces(int64_t max_N, int64_t max_K, torch::Device device) {
   TORCH_CHECK(device.is_cuda(), "init_workspaces: device must be a GPU");
   size_t need = 0;
   for (int bits = 1; bits <= 4; ++bits) {
-    for (int64_t M = 1; M <= 32; ++M)
-      need = std::max(need, wlq_gemm_workspace_bytes(M, max_N, max_K, bits, device.index()));
-    for (int64_t M = 64; M <= 65536; M *= 2)
-      need = std::max(need, wlq_gemm_workspace_bytes(M, max_N, max_K, bits, device.index()));
+    for (int32_t r : {0, 64}) {
+      for (int64_t M = 1; M <= 32; ++M)
+        need = std::max(need, wlq_gemm_workspace_bytes(M, max_N, max_K, bits, r, device.index()));
+    }
+    for (int64_t M = 64; M <= 16384; M *= 2)
+      need = std::max(need, wlq_gemm_workspace_bytes(M, max_N, max_K, bits, 0, device.index()));
   }
   workspace_for(device, need);
 }
@@ -103,7 +106,8 @@ void gemv_forward(torch::Tensor q_packed, torch::Tensor lut_c, torch::Tensor x, 
                   int64_t K, int64_t bits, c10::optional<torch::Tensor> chunk_offsets,
                   c10::optional<torch::Tensor> chunk_cols, c10::optional<torch::Tensor> chunk_vals,
                   c10::optional<torch::Tensor> lora_B, c10::optional<torch::Tensor> lora_h,
-                  c10::optional<torch::Tensor> dora_gamma, double lora_scale, int64_t group_size) {
+                  c10::optional<torch::Tensor> dora_gamma, double lora_scale, int64_t group_size,
+                  c10::optional<torch::Tensor> lora_A) {
   const torch::Device dev = x.device();
   check_dev(q_packed, "q_packed", dev, torch::kInt32);
   check_dev(lut_c, "lut_c", dev, torch::kFloat16);
@@ -121,24 +125,27 @@ void gemv_forward(torch::Tensor q_packed, torch::Tensor lut_c, torch::Tensor x, 
   const void* B = opt_ptr<void>(lora_B, torch::kFloat16, "lora_B", dev);
   const float* h = opt_ptr<float>(lora_h, torch::kFloat32, "lora_h", dev);
   const void* g = opt_ptr<void>(dora_gamma, torch::kFloat16, "dora_gamma", dev);
+  const void* A = opt_ptr<void>(lora_A, torch::kFloat16, "lora_A", dev);
   const int32_t r = (lora_B.has_value() && lora_B->defined() && lora_B->dim() > 1) ? (int32_t)lora_B->size(1) : 0;
-  if (B && h && g && r > 0) {
+  if (B && g && r > 0 && (h || A)) {
     TORCH_CHECK(lora_B->numel() == N * r, "lora_B must be [N, r]");
-    TORCH_CHECK(lora_h->numel() == r, "lora_h must have r=", r, " elements");
+    if (h) TORCH_CHECK(lora_h->numel() == r, "lora_h must have r=", r, " elements");
+    if (!h) TORCH_CHECK(lora_A->numel() == r * K, "lora_A must be [r, K]");
     TORCH_CHECK(dora_gamma->numel() == N, "dora_gamma must have N elements");
   }
-  const size_t need = wlq_gemm_workspace_bytes(1, N, K, (int32_t)bits, dev.index());
+  const size_t need = wlq_gemm_workspace_bytes(1, N, K, (int32_t)bits, (h || !A) ? 0 : r, dev.index());
   torch::Tensor ws = workspace_for(dev, need);
   check_status(wlq_gemv(q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), x.data_ptr(), out.data_ptr(), offs, cols,
-                        vals, B, h, g, (float)lora_scale, r, N, K, (int32_t)bits, (int32_t)group_size, ws.data_ptr(),
-                        (size_t)ws.numel(), current_stream(dev)));
+                        vals, B, h, g, A, (float)lora_scale, r, N, K, (int32_t)bits, (int32_t)group_size,
+                        ws.data_ptr(), (size_t)ws.numel(), current_stream(dev)));
 }
 
 void gemm_forward(torch::Tensor X, torch::Tensor q_packed, torch::Tensor lut_c, torch::Tensor out, int64_t N,
                   int64_t K, int64_t bits, int64_t words_per_row, c10::optional<torch::Tensor> chunk_offsets,
                   c10::optional<torch::Tensor> chunk_cols, c10::optional<torch::Tensor> chunk_vals,
                   c10::optional<torch::Tensor> lora_H, c10::optional<torch::Tensor> lora_B,
-                  c10::optional<torch::Tensor> dora_gamma, double lora_scale, int64_t group_size) {
+                  c10::optional<torch::Tensor> dora_gamma, double lora_scale, int64_t group_size,
+                  c10::optional<torch::Tensor> lora_A) {
   const torch::Device dev = X.device();
   check_dev(X, "X", dev, torch::kFloat16);
   check_dev(q_packed, "q_packed", dev, torch::kInt32);
@@ -157,16 +164,18 @@ void gemm_forward(torch::Tensor X, torch::Tensor q_packed, torch::Tensor lut_c, 
   const float* H = opt_ptr<float>(lora_H, torch::kFloat32, "lora_H", dev);
   const void* B = opt_ptr<void>(lora_B, torch::kFloat16, "lora_B", dev);
   const void* g = opt_ptr<void>(dora_gamma, torch::kFloat16, "dora_gamma", dev);
+  const void* A = opt_ptr<void>(lora_A, torch::kFloat16, "lora_A", dev);
   const int32_t r = (lora_B.has_value() && lora_B->defined() && lora_B->dim() > 1) ? (int32_t)lora_B->size(1) : 0;
-  if (B && H && g && r > 0) {
+  if (B && g && r > 0 && (H || A)) {
     TORCH_CHECK(lora_B->numel() == N * r, "lora_B must be [N, r]");
-    TORCH_CHECK(lora_H->numel() == M * r, "lora_H must be [M, r]");
+    if (H) TORCH_CHECK(lora_H->numel() == M * r, "lora_H must be [M, r]");
+    if (!H) TORCH_CHECK(lora_A->numel() == r * K, "lora_A must be [r, K]");
     TORCH_CHECK(dora_gamma->numel() == N, "dora_gamma must have N elements");
   }
-  const size_t need = wlq_gemm_workspace_bytes(M, N, K, (int32_t)bits, dev.index());
+  const size_t need = wlq_gemm_workspace_bytes(M, N, K, (int32_t)bits, (H || !A) ? 0 : r, dev.index());
   torch::Tensor ws = workspace_for(dev, need);
   check_status(wlq_gemm(X.data_ptr(), q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), out.data_ptr(), M, N, K,
-                        (int32_t)bits, words_per_row, (int32_t)group_size, offs, cols, vals, H, B, g,
+                        (int32_t)bits, words_per_row, (int32_t)group_size, offs, cols, vals, H, B, g, A,
                         (float)lora_scale, r, ws.data_ptr(), (size_t)ws.numel(), current_stream(dev)));
 }
 
@@ -242,10 +251,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("lut_c"), py::arg("x"), py::arg("out"), py::arg("N"), py::arg("K"), py::arg("bits"),
         py::arg("chunk_offsets") = py::none(), py::arg("chunk_cols") = py::none(), py::arg("chunk_vals") = py::none(),
         py::arg("lora_B") = py::none(), py::arg("lora_h") = py::none(), py::arg("dora_gamma") = py::none(),
-        py::arg("lora_scale") = 1.0, py::arg("group_size") = 0);
+        py::arg("lora_scale") = 1.0, py::arg("group_size") = 0, py::arg("lora_A") = py::none());
   m.def("gemm_forward", &gemm_forward, "WLQ product for M activation rows", py::arg("X"), py::arg("q_packed"),
         py::arg("lut_c"), py::arg("out"), py::arg("N"), py::arg("K"), py::arg("bits"), py::arg("words_per_row"),
         py::arg("chunk_offsets") = py::none(), py::arg("chunk_cols") = py::none(), py::arg("chunk_vals") = py::none(),
         py::arg("lora_H") = py::none(), py::arg("lora_B") = py::none(), py::arg("dora_gamma") = py::none(),
-        py::arg("lora_scale") = 1.0, py::arg("group_size") = 0);
+        py::arg("lora_scale") = 1.0, py::arg("group_size") = 0, py::arg("lora_A") = py::none());
 }

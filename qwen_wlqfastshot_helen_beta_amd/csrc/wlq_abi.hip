@@ -114,11 +114,13 @@ int make_layer(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K,
   return WLQ_OK;
 }
 
-wlq::Dora make_dora(const void* lora_B, const float* lora_H, const void* dora_gamma, float scale, int32_t r) {
+wlq::Dora make_dora(const void* lora_B, const float* lora_H, const void* dora_gamma, const void* lora_A,
+                    float scale, int32_t r) {
   wlq::Dora D{};
-  if (lora_B != nullptr && lora_H != nullptr && dora_gamma != nullptr && r > 0) {
+  if (lora_B != nullptr && dora_gamma != nullptr && r > 0 && (lora_H != nullptr || lora_A != nullptr)) {
     D.B = reinterpret_cast<const uint16_t*>(lora_B);
     D.H = lora_H;
+    D.A = lora_H != nullptr ? nullptr : reinterpret_cast<const uint16_t*>(lora_A);
     D.gamma = reinterpret_cast<const uint16_t*>(dora_gamma);
     D.scale = scale;
     D.r = r;
@@ -126,7 +128,9 @@ wlq::Dora make_dora(const void* lora_B, const float* lora_H, const void* dora_ga
   return D;
 }
 
-int run_product(const wlq::Layer& L, const wlq::Dora& D, const void* X, void* out, int64_t M, void* workspace,
+size_t round_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int run_product(const wlq::Layer& L, wlq::Dora D, const void* X, void* out, int64_t M, void* workspace,
                 size_t workspace_bytes, hipStream_t stream, const char* fn) {
   if (M < 0 || M > 0x7fffffff / 4) {
     wlq::set_error("%s: bad M=%lld", fn, (long long)M);
@@ -139,11 +143,34 @@ int run_product(const wlq::Layer& L, const wlq::Dora& D, const void* X, void* ou
   }
   const int cus = current_cu_count();
   size_t ws = workspace != nullptr ? workspace_bytes : 0;
+  char* wbase = reinterpret_cast<char*>(workspace);
   const uint16_t* x = reinterpret_cast<const uint16_t*>(X);
   uint16_t* y = reinterpret_cast<uint16_t*>(out);
-  float* w = reinterpret_cast<float*>(workspace);
-  if (M <= wlq::skinny_max_m()) {
-    const wlq::SplitPlan p = wlq::plan_skinny(L, (int)M, cus, ws);
+  const bool skinny = M <= wlq::skinny_max_m();
+  const bool need_h = D.r > 0 && D.H == nullptr;
+  const bool fused_h = need_h && skinny && D.r <= wlq::skinny_max_fused_rank();
+  if (need_h && !fused_h) {  // H = fp16(X A^T) computed first into the front of the workspace
+    const size_t hb = round_up((size_t)M * D.r * sizeof(float));
+    if (ws < hb) {
+      wlq::set_error("%s: computing H from lora_A needs a workspace of at least %zu bytes", fn, hb);
+      return WLQ_ERR_CAPACITY;
+    }
+    float* H = reinterpret_cast<float*>(wbase);
+    int st = hip_status(wlq::launch_lora_h(x, D.A, (int)M, L.K, D.r, H, stream), fn);
+    if (st != WLQ_OK) return st;
+    D.H = H;
+    D.A = nullptr;
+    wbase += hb;
+    ws -= hb;
+  }
+  float* w = reinterpret_cast<float*>(wbase);
+  if (skinny) {
+    const wlq::SplitPlan p = wlq::plan_skinny(L, (int)M, cus, ws, fused_h ? D.r : 0);
+    if (p.workspace_bytes > ws) {
+      wlq::set_error("%s: the fused DoRA path needs a workspace of at least %zu bytes (got %zu)", fn,
+                     p.workspace_bytes, ws);
+      return WLQ_ERR_CAPACITY;
+    }
     return hip_status(wlq::launch_skinny(L, D, x, y, (int)M, p, w, stream), fn);
   }
   const wlq::SplitPlan p = wlq::plan_gemm(L, (int)M, cus, ws);
@@ -154,7 +181,7 @@ int run_product(const wlq::Layer& L, const wlq::Dora& D, const void* X, void* ou
 
 extern "C" {
 
-size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, int32_t device) {
+size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, int32_t r, int32_t device) {
   if (bits < 1 || bits > 4 || M <= 0 || N <= 0 || K < 0) return 0;
   wlq::Layer L{};
   L.N = (int)N;
@@ -165,33 +192,36 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
   L.nch = (int)((K + L.chunk - 1) / L.chunk);
   const int cus = device >= 0 ? cu_count_for(device) : current_cu_count();
   const size_t unlimited = ~(size_t)0;
-  const wlq::SplitPlan p = (M <= wlq::skinny_max_m()) ? wlq::plan_skinny(L, (int)M, cus, unlimited)
-                                                       : wlq::plan_gemm(L, (int)M, cus, unlimited);
-  return p.workspace_bytes;
+  const bool skinny = M <= wlq::skinny_max_m();
+  const bool fused = skinny && r > 0 && r <= wlq::skinny_max_fused_rank();
+  const size_t hb = (r > 0 && !fused) ? round_up((size_t)M * r * sizeof(float)) : 0;
+  const wlq::SplitPlan p = skinny ? wlq::plan_skinny(L, (int)M, cus, unlimited, fused ? r : 0)
+                                  : wlq::plan_gemm(L, (int)M, cus, unlimited);
+  return hb + p.workspace_bytes;
 }
 
 int wlq_gemv(const int32_t* q_packed, const void* lut_c, const void* x, void* out, const int32_t* chunk_offsets,
              const uint16_t* chunk_cols, const uint8_t* chunk_vals, const void* lora_B, const float* lora_h,
-             const void* dora_gamma, float lora_scale, int32_t r, int64_t N, int64_t K, int32_t bits,
-             int32_t group_size, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+             const void* dora_gamma, const void* lora_A, float lora_scale, int32_t r, int64_t N, int64_t K,
+             int32_t bits, int32_t group_size, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   wlq::Layer L{};
   int st = make_layer(q_packed, lut_c, N, K, bits, -1, group_size, chunk_offsets, chunk_cols, chunk_vals,
                       "wlq_gemv", &L);
   if (st != WLQ_OK) return st;
-  const wlq::Dora D = make_dora(lora_B, lora_h, dora_gamma, lora_scale, r);
+  const wlq::Dora D = make_dora(lora_B, lora_h, dora_gamma, lora_A, lora_scale, r);
   return run_product(L, D, x, out, 1, workspace, workspace_bytes, stream, "wlq_gemv");
 }
 
 int wlq_gemm(const void* X, const int32_t* q_packed, const void* lut_c, void* out, int64_t M, int64_t N, int64_t K,
              int32_t bits, int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets,
              const uint16_t* chunk_cols, const uint8_t* chunk_vals, const float* lora_H, const void* lora_B,
-             const void* dora_gamma, float lora_scale, int32_t r, void* workspace, size_t workspace_bytes,
-             hipStream_t stream) {
+             const void* dora_gamma, const void* lora_A, float lora_scale, int32_t r, void* workspace,
+             size_t workspace_bytes, hipStream_t stream) {
   wlq::Layer L{};
   int st = make_layer(q_packed, lut_c, N, K, bits, words_per_row, group_size, chunk_offsets, chunk_cols, chunk_vals,
                       "wlq_gemm", &L);
   if (st != WLQ_OK) return st;
-  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_scale, r);
+  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_A, lora_scale, r);
   return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, "wlq_gemm");
 }
 
@@ -216,7 +246,7 @@ int wlq_dora_epilogue(void* out, const float* lora_H, const void* lora_B, const 
     wlq::set_error("wlq_dora_epilogue: bad shape M=%lld N=%lld", (long long)M, (long long)N);
     return WLQ_ERR_BAD_SHAPE;
   }
-  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_scale, r);
+  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, nullptr, lora_scale, r);
   if (M == 0 || N == 0 || D.r == 0) return WLQ_OK;
   if (out == nullptr) {
     wlq::set_error("wlq_dora_epilogue: out must be non-null");

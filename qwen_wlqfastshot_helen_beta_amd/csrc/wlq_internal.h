@@ -21,10 +21,12 @@ struct Layer {
 };
 
 // DoRA epilogue operands: y = (acc + scale * H[i,:] . B[n,:]) * gamma[n].
+// H is given by the caller, or computed from A as fp16(x . A^T) when H is null.
 struct Dora {
   const uint16_t* B;        // fp16 [N, r]
-  const float* H;           // fp32 [M, r]
+  const float* H;           // fp32 [M, r] or nullptr
   const uint16_t* gamma;    // fp16 [N]
+  const uint16_t* A;        // fp16 [r, K] (lora_A) or nullptr
   float scale;
   int r;                    // 0 disables the epilogue
 };
@@ -38,7 +40,9 @@ struct SplitPlan {
 
 int slab_cols(int bits);             // columns one 16-row wave tile covers per step
 int skinny_max_m();
-SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_bytes);
+int skinny_max_fused_rank();         // largest DoRA rank whose H the decode kernel computes itself
+// fused_rank > 0: H will be computed from lora_A inside the decode product.
+SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_bytes, int fused_rank);
 hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint16_t* out, int M,
                          const SplitPlan& plan, float* workspace, hipStream_t stream);
 
@@ -51,6 +55,14 @@ hipError_t launch_dequant(const Layer& L, uint16_t* W, hipStream_t stream);
 // Sum of fp32 split-K partials [splits, M, N] followed by the DoRA epilogue.
 hipError_t launch_splitk_reduce(const float* partial, int splits, int M, int N, const Dora& D, uint16_t* out,
                                 hipStream_t stream);
+
+// Decode finish: sum split partials, round the DoRA H (from hpart partial sums
+// over h_blocks column blocks, or D.H) and apply the epilogue.
+hipError_t launch_finalize(const float* partial, int splits, int M, int N, const Dora& D, const float* hpart,
+                           int h_blocks, uint16_t* out, hipStream_t stream);
+
+// H[M, r] = fp32(fp16(X . A^T)) (the reference's F.linear in fp16, then .float()).
+hipError_t launch_lora_h(const uint16_t* X, const uint16_t* A, int M, int K, int r, float* H, hipStream_t stream);
 
 // In-place epilogue on an fp16 output (the reference's separate pass).
 hipError_t launch_dora_epilogue(uint16_t* out, int M, int N, const Dora& D, hipStream_t stream);

@@ -5,21 +5,37 @@
 // (csrc/gemm_kernel.cu:32-294) for 2 <= M < 16, plus the M >= 16 dequant+HGEMM
 // path (csrc/vllm_binding.cpp:355-393) for M <= 32.
 //
-// Work decomposition.  A block is 4 waves; wave w owns a 16-row tile of W, the
-// block owns a contiguous range of K "slabs" (4 code windows = 128 columns for
-// 4-bit).  Per slab, lane l = r + 16*kq streams one 16-byte code window of row
-// r (columns kq*WIN .. +WIN of the slab), dequantizes it through its LUT byte
-// planes and feeds V_MFMA_F32_16X16X32_F16 as the B operand; the A operand is the
-// activation block (rows 16*mt + r) read from LDS, where it was staged in the
-// same column order P.  The 16x16 accumulator keeps the whole K reduction in the
-// matrix core; no cross-lane reduction is needed for the dense part.
+// Work decomposition.  The grid is one-dimensional: first the DoRA blocks (one
+// per 512 columns, computing partial x.A^T sums with MFMA when the caller did
+// not pass H), then row_blocks x splits product blocks.  A product block is 4
+// waves; wave w owns a 16-row tile of W and the block owns a contiguous range
+// of K "slabs" (4 code windows, 128 columns for 4-bit).  Per slab, lane
+// l = r + 16*kq takes one 16-byte code window of row r (columns kq*WIN..+WIN of
+// the slab), dequantizes it through its LUT byte planes and feeds
+// V_MFMA_F32_16X16X32_F16 as the B operand; the A operand (activation rows
+// 16*mt + r) comes from LDS, staged in the same column order P.  The 16x16
+// accumulator keeps the K reduction inside the matrix core.
 //
-// Outliers use the delta form of the reference GEMV (csrc/gemv_kernel.cu:262-288):
-// after the dense loop each lane walks every 4th CSR entry of its row in the
-// block's column range and accumulates (w_true - lut[code]) * x[i, col] for all
-// activation rows; the four lanes of a row are summed with two xor-shuffles.
-// Split-K partials go to an fp32 workspace and a second kernel applies the
-// DoRA epilogue; otherwise the epilogue runs here.
+// 4-bit fast path, pipelined per 512-column outlier chunk (= 4 slabs): the code
+// windows and LUT quarters of the next chunk are loaded while the current one
+// is consumed (unconditional loads, so HBM latency overlaps the dequant/MFMA
+// work); each of the four lanes of a row loads one quarter (4 entries) of the
+// row's group LUT, splits it into byte planes and the lanes exchange planes
+// through wave-private LDS, so a 16-entry LUT costs one 8-byte load and two
+// perms per lane.  The chunk's code windows and LUT planes stay in LDS tiles,
+// and the chunk's outliers are applied right after its four slabs in the delta
+// form of the reference GEMV (csrc/gemv_kernel.cu:262-288): each lane takes
+// every 4th CSR entry of its row and accumulates (w_true - lut[code]) * x[i, col]
+// with code and LUT value read from the tiles; CSR offsets are fetched two
+// chunks ahead and entries one chunk ahead.  The four lanes of a row are summed
+// with two xor-shuffles at the end.  Other widths (generic kernel) walk the
+// block's CSR entries after the dense loop with global loads.
+//
+// Output: with one split and H supplied by the caller the epilogue
+// fp16_rn((acc + s * H.B) * gamma) runs here; otherwise fp32 partials go to
+// the workspace and finalize_kernel (wlq_epilogue.hip) sums splits and DoRA
+// partials, rounds H to fp16 (the reference's F.linear output type) and applies
+// the epilogue.
 #include <algorithm>
 #include <utility>
 
@@ -34,26 +50,32 @@ constexpr int kRowsPerBlock = 16 * kWaves;
 constexpr int kXStageBytes = 32768;  // activation staging budget per block
 constexpr int kMaxM = 32;
 constexpr int kMaxSplits = 64;
+constexpr int kPF = 4;               // slabs in flight per wave (4-bit path)
+constexpr int kHCols = 512;          // columns per DoRA block
+constexpr int kMaxFusedRank = 64;
 
 struct SkinnyArgs {
   const uint32_t* q;
   const uint16_t* lut;
   const uint16_t* x;
   uint16_t* out;
-  float* partial;
+  float* partial;   // [splits, M, N]
+  float* hpart;     // [h_blocks, M, r] (fused DoRA) or nullptr
   const int32_t* offsets;
   const uint16_t* cols;
   const uint8_t* vals;
   const uint16_t* B;
   const float* H;
   const uint16_t* gamma;
+  const uint16_t* A;  // lora_A [r, K] for the fused path
   float scale;
   int r;
   int M, N, K, wpr, G, ng, nch, chunk;
   uint32_t g_magic;  // floor(2^32 / G) + 1: floor(c / G) == umulhi(c, g_magic) for c < 2^20, G < 4096
-  int slabs_per_split, seg_slabs, xstride, splits;
+  int slabs_per_split, seg_slabs, xstride, splits, row_blocks, h_blocks;
   int x_vec;         // 16-byte loads of x rows are aligned
   int has_csr;
+  int direct_out;    // epilogue in this kernel (one split, H given)
 };
 
 __device__ __forceinline__ int group_of(int col, uint32_t magic) { return (int)__umulhi((uint32_t)col, magic); }
@@ -84,13 +106,158 @@ __device__ __forceinline__ void stage_x(const SkinnyArgs& a, uint16_t* xs, int c
   }
 }
 
+// 16-byte load of 8 fp16 starting at column k of a row of length K (zeros past K).
+__device__ __forceinline__ u32x4_t load8(const uint16_t* row, int k, int K, bool vec) {
+  u32x4_t v = {0u, 0u, 0u, 0u};
+  if (vec && k + 8 <= K) return *reinterpret_cast<const u32x4_t*>(row + k);
+  uint32_t e[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) e[j] = (k + j < K) ? (uint32_t)row[k + j] : 0u;
+  v.x = e[0] | (e[1] << 16);
+  v.y = e[2] | (e[3] << 16);
+  v.z = e[4] | (e[5] << 16);
+  v.w = e[6] | (e[7] << 16);
+  return v;
+}
+
+// DoRA block hb: hpart[hb, i, j] = sum over columns [hb*512, +512) of x[i, k] * A[j, k]
+// for i < M, j < r, with MFMA 16x16x32 (both operands in natural k order).
+// Wave w covers 128 columns; the four wave partials are summed through LDS.
+template <int MT>
+__device__ void dora_h_block(const SkinnyArgs& a, int hb, float* red) {
+  constexpr int JT = kMaxFusedRank / 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int jt_n = (a.r + 15) >> 4;
+  const bool vec = a.x_vec != 0;
+  const bool avec = ((reinterpret_cast<uintptr_t>(a.A) & 15u) == 0) && (a.K % 8) == 0;
+  float4_t acc[MT][JT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) acc[mt][jt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const int kbase = hb * kHCols + wave * 128;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int k = kbase + 32 * ks + 8 * kq;
+    u32x4_t xa[MT], ab[JT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int i = 16 * mt + r16;
+      xa[mt] = (i < a.M && k < a.K) ? load8(a.x + (size_t)i * a.K, k, a.K, vec) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) {
+      const int j = 16 * jt + r16;
+      ab[jt] = (jt < jt_n && j < a.r && k < a.K) ? load8(a.A + (size_t)j * a.K, k, a.K, avec)
+                                                 : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt)
+        if (jt < jt_n) acc[mt][jt] = mfma16x16x32(xa[mt], ab[jt], acc[mt][jt]);
+  }
+  // reduce the four waves: red[wave][mt][jt][e][lane]
+  constexpr int per_wave = MT * JT * 4 * 64;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[wave * per_wave + ((mt * JT + jt) * 4 + e) * 64 + lane] = acc[mt][jt][e];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < per_wave; idx += blockDim.x) {
+    const float v = red[idx] + red[per_wave + idx] + red[2 * per_wave + idx] + red[3 * per_wave + idx];
+    const int ln = idx & 63;
+    const int e = (idx >> 6) & 3;
+    const int t = idx >> 8;
+    const int jt = t % JT;
+    const int mt = t / JT;
+    const int i = 16 * mt + 4 * (ln >> 4) + e;
+    const int j = 16 * jt + (ln & 15);
+    if (i < a.M && j < a.r) a.hpart[((size_t)hb * a.M + i) * a.r + j] = v;
+  }
+}
+
+// Delta-form outlier correction for the block's column range, added to the
+// lane's accumulators (see the file comment).
+template <int BITS, int MT, int MB, bool PER_ROW>
+__device__ __forceinline__ void outlier_delta(const SkinnyArgs& a, int n, bool row_ok, int kq, int k_lo, int k_hi,
+                                              const uint32_t* qrow, const uint16_t* lrow, float4_t acc[MT]) {
+  constexpr int NCB = 1 << BITS;
+  float corr[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) corr[i] = 0.f;
+  if (row_ok && k_lo < k_hi) {
+    const int c_lo = k_lo / a.chunk;
+    const int c_hi = min(a.nch, (k_hi + a.chunk - 1) / a.chunk);
+    const int32_t* offr = a.offsets + (size_t)n * (a.nch + 1);
+    for (int c = c_lo; c < c_hi; ++c) {
+      const int s0 = offr[c];
+      const int s1 = offr[c + 1];
+      const int cbase = c * a.chunk;
+      for (int e = s0 + kq; e < s1; e += 4) {
+        const int col = cbase + (int)a.cols[e];
+        if (col >= k_lo && col < k_hi) {
+          const uint32_t code = code_at<BITS>(qrow, col);
+          const int g = PER_ROW ? 0 : min(group_of(col, a.g_magic), a.ng - 1);
+          const float d = h2f((uint16_t)((uint32_t)a.vals[e] << 8)) - h2f(lrow[g * NCB + code]);
+#pragma unroll
+          for (int i = 0; i < MB; ++i)
+            if (i < a.M) corr[i] += d * h2f(a.x[(size_t)i * a.K + col]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    if (i < a.M) {
+      float v = corr[i];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      if (kq == ((i >> 2) & 3)) acc[i >> 4][i & 3] += v;
+    }
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ void write_result(const SkinnyArgs& a, int split, int n, bool row_ok, int kq,
+                                             const float4_t acc[MT]) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * mt + 4 * kq + e;
+      if (i < a.M && row_ok) {
+        float v = acc[mt][e];
+        if (a.direct_out) {
+          if (a.r > 0) {
+            float ls = 0.f;
+            const float* h = a.H + (size_t)i * a.r;
+            const uint16_t* bb = a.B + (size_t)n * a.r;
+            for (int j = 0; j < a.r; ++j) ls += h[j] * h2f(bb[j]);
+            v = (v + a.scale * ls) * h2f(a.gamma[n]);
+          }
+          a.out[(size_t)i * a.N + n] = f2h_rn(v);
+        } else {
+          a.partial[((size_t)split * a.M + i) * a.N + n] = v;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- generic path
+
 template <int BITS>
 struct LaneState {
   LutPlanes<BITS> pl0, pl1;
   int split_col;  // first column served by pl1 (TWO_LUT)
 };
 
-// One 8-column block S of the lane window: dequantize and multiply.
 template <int BITS, int MT, bool TWO_LUT, int S>
 __device__ __forceinline__ void window_block(const uint32_t w[4], const LaneState<BITS>& st, int c0,
                                              const uint16_t* xs, int xstride, int xoff, int r, int M,
@@ -127,24 +294,33 @@ __device__ __forceinline__ void window_all(std::integer_sequence<int, S...>, con
 }
 
 template <int BITS, int MT, int MB, bool PER_ROW, bool TWO_LUT>
-__global__ __launch_bounds__(256) void skinny_kernel(const SkinnyArgs a) {
+__global__ __launch_bounds__(256) void skinny_generic_kernel(const SkinnyArgs a) {
   constexpr int WIN = CodeGeom<BITS>::kWin;
   constexpr int SLAB = 4 * WIN;
   constexpr int NCB = 1 << BITS;
   extern __shared__ __align__(16) uint16_t xs[];
 
+  int bid = blockIdx.x;
+  if (bid < a.h_blocks) {
+    dora_h_block<MT>(a, bid, reinterpret_cast<float*>(xs));
+    return;
+  }
+  bid -= a.h_blocks;
+  const int split = bid / a.row_blocks;
+  const int rb = bid - split * a.row_blocks;
+
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r = lane & 15;
   const int kq = lane >> 4;
-  const int n = blockIdx.x * kRowsPerBlock + wave * 16 + r;
+  const int n = rb * kRowsPerBlock + wave * 16 + r;
   const bool row_ok = n < a.N;
   const int nc = row_ok ? n : (a.N - 1);
   const uint32_t* qrow = a.q + (size_t)nc * a.wpr;
   const uint16_t* lrow = a.lut + (size_t)nc * a.ng * NCB;
 
   const int total_slabs = (a.K + SLAB - 1) / SLAB;
-  const int t_begin = blockIdx.y * a.slabs_per_split;
+  const int t_begin = split * a.slabs_per_split;
   const int t_end = min(total_slabs, t_begin + a.slabs_per_split);
 
   float4_t acc[MT];
@@ -192,33 +368,292 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkinnyArgs a) {
     }
   }
 
-  if (a.has_csr) {
-    float corr[MB];
+  if (a.has_csr)
+    outlier_delta<BITS, MT, MB, PER_ROW>(a, n, row_ok, kq, t_begin * SLAB, min(a.K, t_end * SLAB), qrow, lrow, acc);
+  write_result<MT>(a, split, n, row_ok, kq, acc);
+}
+
+// -------------------------------------------------------------- 4-bit fast path
+
+constexpr int kEB = 4;  // CSR entries per lane fetched ahead for the next chunk
+
+// One prefetched slab: the lane's code window and its LUT quarters.
+template <int NGS>
+struct Stage4 {
+  u32x4_t codes;
+  u32x2_t lq[NGS];  // quarter kq (entries 4kq..4kq+3) of the row's LUT for each group in the slab
+};
+
+// Unconditional load of slab t (callers clamp t to a valid slab; windows past the
+// row end read the row's last window -- those columns meet zero activations).
+template <bool PER_ROW, int NGS>
+__device__ __forceinline__ void stage4_load(Stage4<NGS>& s, const SkinnyArgs& a, const uint32_t* qrow,
+                                            const uint16_t* lrow, int kq, int t) {
+  const int wi = min(t * 16 + kq * 4, a.wpr - 4);
+  s.codes = *reinterpret_cast<const u32x4_t*>(qrow + wi);
+  if constexpr (!PER_ROW) {
+    const int g0 = (NGS > 1) ? t * NGS : group_of(t * 128, a.g_magic);
 #pragma unroll
-    for (int i = 0; i < MB; ++i) corr[i] = 0.f;
-    const int k_lo = t_begin * SLAB;
-    const int k_hi = min(a.K, t_end * SLAB);
-    if (row_ok && k_lo < k_hi) {
-      const int c_lo = k_lo / a.chunk;
-      const int c_hi = min(a.nch, (k_hi + a.chunk - 1) / a.chunk);
-      const int32_t* offr = a.offsets + (size_t)n * (a.nch + 1);
-      for (int c = c_lo; c < c_hi; ++c) {
-        const int s0 = offr[c];
-        const int s1 = offr[c + 1];
-        const int cbase = c * a.chunk;
-        for (int e = s0 + kq; e < s1; e += 4) {
-          const int col = cbase + (int)a.cols[e];
-          if (col >= k_lo && col < k_hi) {
-            const uint32_t code = code_at<BITS>(qrow, col);
-            const int g = PER_ROW ? 0 : min(group_of(col, a.g_magic), a.ng - 1);
-            const float d = h2f((uint16_t)((uint32_t)a.vals[e] << 8)) - h2f(lrow[g * NCB + code]);
+    for (int j = 0; j < NGS; ++j) {
+      const int g = min(g0 + j, a.ng - 1);
+      s.lq[j] = *reinterpret_cast<const u32x2_t*>(lrow + g * 16 + 4 * kq);
+    }
+  }
+}
+
+template <int MT, int S>
+__device__ __forceinline__ void fast_block(const u32x4_t& codes, const LutPlanes<4>& t, const uint16_t* const xp[MT],
+                                           float4_t acc[MT]) {
+  const uint32_t w = S == 0 ? codes.x : S == 1 ? codes.y : S == 2 ? codes.z : codes.w;
+  uint32_t b[4];
+  dequant_word4(w, t, b);
+  u32x4_t bv;
+  bv.x = b[0]; bv.y = b[1]; bv.z = b[2]; bv.w = b[3];
 #pragma unroll
-            for (int i = 0; i < MB; ++i)
-              if (i < a.M) corr[i] += d * h2f(a.x[(size_t)i * a.K + col]);
-          }
-        }
+  for (int mt = 0; mt < MT; ++mt) {
+    const u32x4_t av = *reinterpret_cast<const u32x4_t*>(xp[mt] + 8 * S);
+    acc[mt] = mfma16x16x32(av, bv, acc[mt]);
+  }
+}
+
+// Wave-private LDS tiles of one outlier chunk (4 slabs x 16 rows):
+//   ctile: code windows, [row][slab][kq] x 16 B
+//   ltile: LUT byte planes (lo 16 B | hi 16 B), [row][slab][group] x 32 B
+template <int NGS>
+struct ChunkTiles {
+  uint32_t* ctile;
+  uint32_t* ltile;
+};
+
+template <bool PER_ROW, int NGS, int MT>
+__device__ __forceinline__ void stage4_consume(const Stage4<NGS>& s, int slab_in_chunk, LutPlanes<4>& pl,
+                                               const ChunkTiles<NGS>& tl, int r, int kq,
+                                               const uint16_t* const xp[MT], float4_t acc[MT]) {
+  *reinterpret_cast<u32x4_t*>(tl.ctile + ((r * 4 + slab_in_chunk) * 4 + kq) * 4) = s.codes;
+  if constexpr (!PER_ROW) {
+    // split my LUT quarters into planes and exchange them with the row's other lanes
+#pragma unroll
+    for (int j = 0; j < NGS; ++j) {
+      uint32_t* base = tl.ltile + ((r * 4 + slab_in_chunk) * NGS + j) * 8;
+      base[kq] = perm_b32(s.lq[j].y, s.lq[j].x, 0x06040200u);
+      base[4 + kq] = perm_b32(s.lq[j].y, s.lq[j].x, 0x07050301u);
+    }
+    const int jown = (NGS == 1) ? 0 : (NGS == 2 ? (kq >> 1) : kq);
+    const uint32_t* own = tl.ltile + ((r * 4 + slab_in_chunk) * NGS + jown) * 8;
+    const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(own);
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(own + 4);
+    pl.lo[0] = lo.x; pl.lo[1] = lo.y; pl.lo[2] = lo.z; pl.lo[3] = lo.w;
+    pl.hi[0] = hi.x; pl.hi[1] = hi.y; pl.hi[2] = hi.z; pl.hi[3] = hi.w;
+  }
+  fast_block<MT, 0>(s.codes, pl, xp, acc);
+  fast_block<MT, 1>(s.codes, pl, xp, acc);
+  fast_block<MT, 2>(s.codes, pl, xp, acc);
+  fast_block<MT, 3>(s.codes, pl, xp, acc);
+}
+
+// CSR entries of one chunk for one lane: entries e0 + kq + 4j, j < kEB.  The
+// column and value registers are only combined when used, so the loads stay in
+// flight while the next chunk streams.
+struct ChunkEntries {
+  int e0, e1;          // the row's entry range for the chunk
+  uint16_t col[kEB];   // column inside the chunk (kept narrow: widened only where used)
+  uint8_t val[kEB];    // e5m2 byte
+};
+
+// Loads are unconditional (clamped to entry e1-1, or 0 for an empty range) so that the
+// wait counters stay in program order; cols/vals point at any readable buffer when the
+// layer has no outliers (every range is then empty).
+__device__ __forceinline__ void entries_load(ChunkEntries& E, const uint16_t* cols, const uint8_t* vals, int kq,
+                                             int e0, int e1) {
+  E.e0 = e0;
+  E.e1 = e1;
+#pragma unroll
+  for (int j = 0; j < kEB; ++j) {
+    const int e = min(e0 + kq + 4 * j, max(e1 - 1, 0));
+    E.col[j] = cols[e];
+    E.val[j] = vals[e];
+  }
+}
+
+// Delta corrections of one entry (chunk-local column cl, e5m2 value vb) from the LDS tiles;
+// x_col0 is the first column of the staged activation segment.
+template <int MB, bool PER_ROW, int NGS>
+__device__ __forceinline__ void entry_delta(const SkinnyArgs& a, const ChunkTiles<NGS>& tl, const uint16_t* xs,
+                                            int r, int c, int cl, uint32_t vb, int k_lo, int k_hi, int x_col0,
+                                            float corr[MB]) {
+  const int gcol = c * 512 + cl;
+  if (gcol < k_lo || gcol >= k_hi) return;
+  const int sl = cl >> 7;
+  const uint32_t word = tl.ctile[((r * 4 + sl) * 4 + ((cl >> 5) & 3)) * 4 + ((cl >> 3) & 3)];
+  const uint32_t code = (word >> (4 * (cl & 7))) & 15u;
+  const int gi = PER_ROW ? 0 : (NGS == 1 ? 0 : (NGS == 2 ? ((cl >> 6) & 1) : ((cl >> 5) & 3)));
+  const unsigned char* planes =
+      reinterpret_cast<const unsigned char*>(tl.ltile + (PER_ROW ? r * 8 : ((r * 4 + sl) * NGS + gi) * 8));
+  const uint32_t lutv = (uint32_t)planes[code] | ((uint32_t)planes[16 + code] << 8);
+  const float d = h2f((uint16_t)(vb << 8)) - h2f((uint16_t)lutv);
+  const int xc = gcol - x_col0;  // column inside the staged activation segment
+  const int xi = (xc & ~7) + p_slot(xc & 7);
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+    if (i < a.M) corr[i] += d * h2f(xs[i * a.xstride + xi]);
+}
+
+template <int MB, bool PER_ROW, int NGS>
+__device__ __forceinline__ void chunk_outliers(const SkinnyArgs& a, const ChunkEntries& E, const ChunkTiles<NGS>& tl,
+                                               const uint16_t* xs, int r, int kq, int c, int k_lo, int k_hi,
+                                               int x_col0, float corr[MB]) {
+#pragma unroll
+  for (int j = 0; j < kEB; ++j) {
+    const bool have = E.e0 + kq + 4 * j < E.e1;
+    if (__ballot(have)) {
+      if (have) entry_delta<MB, PER_ROW, NGS>(a, tl, xs, r, c, (int)E.col[j], (uint32_t)E.val[j], k_lo, k_hi, x_col0, corr);
+    }
+  }
+  // rows with more than 4 * kEB entries in the chunk: fetch the rest directly
+  for (int e = E.e0 + kq + 4 * kEB; e < E.e1; e += 4)
+    entry_delta<MB, PER_ROW, NGS>(a, tl, xs, r, c, (int)a.cols[e], (uint32_t)a.vals[e], k_lo, k_hi, x_col0, corr);
+}
+
+constexpr int kOT = 17;  // chunk offsets per row kept in LDS (16 chunks = 64 slabs per block)
+
+template <int MT, int MB, bool PER_ROW, int NGS>
+__global__ __launch_bounds__(256) void skinny4_kernel(const SkinnyArgs a) {
+  constexpr int SLAB = 128;
+  extern __shared__ __align__(16) uint16_t smem[];
+  // LDS: [x staging: M * xstride halves][64 B zeros]
+  //      [per wave: ctile 4 KB | ltile (PER_ROW ? 512 B : NGS * 2 KB) | otile 16 x kOT ints]
+  uint16_t* xs = smem;
+
+  int bid = blockIdx.x;
+  if (bid < a.h_blocks) {
+    dora_h_block<MT>(a, bid, reinterpret_cast<float*>(smem));
+    return;
+  }
+  bid -= a.h_blocks;
+  const int split = bid / a.row_blocks;
+  const int rb = bid - split * a.row_blocks;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;
+  const int kq = lane >> 4;
+  const int n = rb * kRowsPerBlock + wave * 16 + r;
+  const bool row_ok = n < a.N;
+  const int nc = row_ok ? n : (a.N - 1);
+  const uint32_t* qrow = a.q + (size_t)nc * a.wpr;
+  const uint16_t* lrow = a.lut + (size_t)nc * a.ng * 16;
+
+  const size_t xbytes = ((size_t)a.M * a.xstride * 2 + 15) & ~(size_t)15;
+  uint16_t* zpad = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(smem) + xbytes);
+  constexpr int kLtWords = PER_ROW ? 16 * 8 : 16 * 4 * NGS * 8;
+  constexpr int kWaveWords = 16 * 4 * 4 * 4 + kLtWords + 16 * kOT;
+  uint32_t* wave_lds = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(zpad) + 64) + wave * kWaveWords;
+  ChunkTiles<NGS> tl{wave_lds, wave_lds + 16 * 4 * 4 * 4};
+  int* otile = reinterpret_cast<int*>(wave_lds + 16 * 4 * 4 * 4 + kLtWords) + r * kOT;
+
+  const int total_slabs = (a.K + SLAB - 1) / SLAB;
+  const int t_begin = split * a.slabs_per_split;  // a multiple of 4 (chunk aligned)
+  const int t_end = min(total_slabs, t_begin + a.slabs_per_split);
+  const int k_lo = t_begin * SLAB;
+  const int k_hi = min(a.K, t_end * SLAB);
+  const int c_begin = t_begin >> 2;
+  const int c_end = (t_end + 3) >> 2;
+  const int nchunks = c_end - c_begin;  // <= kOT - 1 (the planner bounds the split)
+
+  float4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float corr[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) corr[i] = 0.f;
+  const bool csr = a.has_csr != 0 && t_begin < t_end;
+
+  LutPlanes<4> pl;
+  if constexpr (PER_ROW) {
+    LutRaw<4> raw;
+    lut_load<4>(raw, lrow);
+    pl = lut_planes<4>(raw);
+    if (kq == 0) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        tl.ltile[r * 8 + p] = pl.lo[p];
+        tl.ltile[r * 8 + 4 + p] = pl.hi[p];
       }
     }
+  }
+  if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zpad)[threadIdx.x] = 0u;
+  // the row's chunk offsets for the block's range, once (all zero without outliers)
+  if (csr) {
+    const int32_t* offr = a.offsets + (size_t)nc * (a.nch + 1) + c_begin;
+    for (int j = kq; j <= nchunks; j += 4) otile[j] = offr[j];
+  } else {
+    for (int j = kq; j <= nchunks; j += 4) otile[j] = 0;
+  }
+
+  // prologue: codes of the first chunk, activations, entries of the first chunk
+  Stage4<NGS> st[4];
+  const int t_last = max(t_end - 1, t_begin);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) stage4_load<PER_ROW, NGS>(st[j], a, qrow, lrow, kq, min(t_begin + j, t_last));
+  int seg0 = t_begin;
+  int seg_end = min(t_end, t_begin + a.seg_slabs);
+  stage_x(a, xs, seg0 * SLAB, (seg_end - seg0) * SLAB);
+  __syncthreads();
+  // A row with entries in the range reads only entries below its last offset; a row
+  // without any reads word 0 of its codes instead (the CSR arrays may then be empty).
+  const bool any = otile[nchunks] > otile[0];
+  const uint16_t* colp = any ? a.cols : reinterpret_cast<const uint16_t*>(a.q);
+  const uint8_t* valp = any ? a.vals : reinterpret_cast<const uint8_t*>(a.q);
+  ChunkEntries ea, eb;
+  entries_load(ea, colp, valp, kq, otile[0], otile[min(1, nchunks)]);
+
+  // one chunk: entries of the next chunk are requested, the four slabs consumed (each
+  // slab's codes re-requested four slabs ahead), then this chunk's outliers applied
+  auto chunk = [&](int c, const ChunkEntries& cur, ChunkEntries& nxt) {
+    const int lc = c - c_begin;
+    entries_load(nxt, colp, valp, kq, otile[min(lc + 1, nchunks)], otile[min(lc + 2, nchunks)]);
+    const int t0 = 4 * c;
+    const uint16_t* xp[MT];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int t = t0 + s;
+      if (t < t_end) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          xp[mt] = (16 * mt + r < a.M) ? xs + (16 * mt + r) * a.xstride + (t - seg0) * SLAB + kq * 32 : zpad;
+        stage4_consume<PER_ROW, NGS, MT>(st[s], s, pl, tl, r, kq, xp, acc);
+      }
+      stage4_load<PER_ROW, NGS>(st[s], a, qrow, lrow, kq, min(t + 4, t_last));
+    }
+    if (csr && row_ok) chunk_outliers<MB, PER_ROW, NGS>(a, cur, tl, xs, r, kq, c, k_lo, k_hi, seg0 * SLAB, corr);
+  };
+
+  if (a.seg_slabs >= a.slabs_per_split) {
+    for (int c = c_begin; c < c_end; c += 2) {  // two chunks per trip: the entry registers alternate
+      chunk(c, ea, eb);
+      if (c + 1 < c_end) chunk(c + 1, eb, ea);
+    }
+  } else {
+    auto restage = [&](int c) {
+      if (4 * c >= seg_end) {  // next activation segment (segments are whole chunks)
+        __syncthreads();
+        seg0 = 4 * c;
+        seg_end = min(t_end, seg0 + a.seg_slabs);
+        stage_x(a, xs, seg0 * SLAB, (seg_end - seg0) * SLAB);
+        __syncthreads();
+      }
+    };
+    for (int c = c_begin; c < c_end; c += 2) {
+      restage(c);
+      chunk(c, ea, eb);
+      if (c + 1 < c_end) {
+        restage(c + 1);
+        chunk(c + 1, eb, ea);
+      }
+    }
+  }
+
+  if (a.has_csr) {
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
       if (i < a.M) {
@@ -229,54 +664,45 @@ __global__ __launch_bounds__(256) void skinny_kernel(const SkinnyArgs a) {
       }
     }
   }
-
-  const bool fused = a.splits == 1;
-  const int n_out = n;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 16 * mt + 4 * kq + e;
-      if (i < a.M && row_ok) {
-        float v = acc[mt][e];
-        if (fused) {
-          if (a.r > 0) {
-            float ls = 0.f;
-            const float* h = a.H + (size_t)i * a.r;
-            const uint16_t* bb = a.B + (size_t)n_out * a.r;
-            for (int j = 0; j < a.r; ++j) ls += h[j] * h2f(bb[j]);
-            v = (v + a.scale * ls) * h2f(a.gamma[n_out]);
-          }
-          a.out[(size_t)i * a.N + n_out] = f2h_rn(v);
-        } else {
-          a.partial[((size_t)blockIdx.y * a.M + i) * a.N + n_out] = v;
-        }
-      }
-    }
-  }
+  write_result<MT>(a, split, n, row_ok, kq, acc);
 }
 
-template <int BITS, int MT, int MB, bool PER_ROW, bool TWO_LUT>
-hipError_t launch_variant(const SkinnyArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((skinny_kernel<BITS, MT, MB, PER_ROW, TWO_LUT>), grid, dim3(256), lds, stream, a);
+// ------------------------------------------------------------------- dispatch
+
+template <int MT, int MB>
+hipError_t launch_fast(const SkinnyArgs& a, int ngs, dim3 grid, size_t lds, hipStream_t stream) {
+  if (a.G <= 0 || a.ng == 1)
+    hipLaunchKernelGGL((skinny4_kernel<MT, MB, true, 1>), grid, dim3(256), lds, stream, a);
+  else if (ngs == 1)
+    hipLaunchKernelGGL((skinny4_kernel<MT, MB, false, 1>), grid, dim3(256), lds, stream, a);
+  else if (ngs == 2)
+    hipLaunchKernelGGL((skinny4_kernel<MT, MB, false, 2>), grid, dim3(256), lds, stream, a);
+  else
+    hipLaunchKernelGGL((skinny4_kernel<MT, MB, false, 4>), grid, dim3(256), lds, stream, a);
   return hipGetLastError();
 }
 
 template <int BITS, int MT, int MB>
-hipError_t launch_lut_mode(const SkinnyArgs& a, int mode, dim3 grid, size_t lds, hipStream_t stream) {
+hipError_t launch_generic(const SkinnyArgs& a, int mode, dim3 grid, size_t lds, hipStream_t stream) {
   switch (mode) {
-    case 0: return launch_variant<BITS, MT, MB, true, false>(a, grid, lds, stream);
-    case 1: return launch_variant<BITS, MT, MB, false, false>(a, grid, lds, stream);
-    default: return launch_variant<BITS, MT, MB, false, true>(a, grid, lds, stream);
+    case 0: hipLaunchKernelGGL((skinny_generic_kernel<BITS, MT, MB, true, false>), grid, dim3(256), lds, stream, a); break;
+    case 1: hipLaunchKernelGGL((skinny_generic_kernel<BITS, MT, MB, false, false>), grid, dim3(256), lds, stream, a); break;
+    default: hipLaunchKernelGGL((skinny_generic_kernel<BITS, MT, MB, false, true>), grid, dim3(256), lds, stream, a); break;
   }
+  return hipGetLastError();
 }
 
-template <int BITS>
-hipError_t launch_bits(const SkinnyArgs& a, int mode, dim3 grid, size_t lds, hipStream_t stream) {
-  if (a.M == 1) return launch_lut_mode<BITS, 1, 1>(a, mode, grid, lds, stream);
-  if (a.M <= 4) return launch_lut_mode<BITS, 1, 4>(a, mode, grid, lds, stream);
-  if (a.M <= 16) return launch_lut_mode<BITS, 1, 16>(a, mode, grid, lds, stream);
-  return launch_lut_mode<BITS, 2, 32>(a, mode, grid, lds, stream);
+template <int MT, int MB>
+hipError_t launch_m(const SkinnyArgs& a, int bits, int mode, bool fast, int ngs, dim3 grid, size_t lds,
+                    hipStream_t stream) {
+  switch (bits) {
+    case 1: return launch_generic<1, MT, MB>(a, mode, grid, lds, stream);
+    case 2: return launch_generic<2, MT, MB>(a, mode, grid, lds, stream);
+    case 3: return launch_generic<3, MT, MB>(a, mode, grid, lds, stream);
+    default:
+      if (!fast) return launch_generic<4, MT, MB>(a, mode, grid, lds, stream);
+      return launch_fast<MT, MB>(a, ngs, grid, lds, stream);
+  }
 }
 
 int window_cols(int bits) { return bits == 4 ? 32 : bits == 3 ? 40 : bits == 2 ? 64 : 128; }
@@ -285,8 +711,9 @@ int window_cols(int bits) { return bits == 4 ? 32 : bits == 3 ? 40 : bits == 2 ?
 
 int slab_cols(int bits) { return 4 * window_cols(bits); }
 int skinny_max_m() { return kMaxM; }
+int skinny_max_fused_rank() { return kMaxFusedRank; }
 
-SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_bytes) {
+SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_bytes, int fused_rank) {
   SplitPlan p{};
   const int slab = slab_cols(L.bits);
   const int total = std::max(1, (L.K + slab - 1) / slab);
@@ -295,16 +722,24 @@ SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_byte
   int splits = std::max(1, (target + row_blocks - 1) / row_blocks);
   splits = std::min(splits, std::min(total, kMaxSplits));
   const size_t per_split = (size_t)M * (size_t)L.N * sizeof(float);
-  while (splits > 1 && (size_t)splits * per_split > workspace_bytes) --splits;
+  const size_t hbytes = fused_rank > 0 ? (size_t)((L.K + kHCols - 1) / kHCols) * M * fused_rank * sizeof(float) : 0;
+  const bool need_partials = fused_rank > 0;  // the fused DoRA path always finishes in finalize
+  while (splits > 1 && (size_t)splits * per_split + hbytes > workspace_bytes) --splits;
   int sps = (total + splits - 1) / splits;
   const int spc = std::max(1, L.chunk / slab);
   if (sps >= spc) sps = (sps + spc - 1) / spc * spc;
+  if (L.bits == 4) {  // whole outlier chunks, at most 16 per block (their offsets are staged in LDS)
+    sps = std::max(kPF, (sps + kPF - 1) / kPF * kPF);
+    sps = std::min(sps, 64);
+  }
   splits = (total + sps - 1) / sps;
   p.splits = splits;
   p.slabs_per_split = sps;
   const int seg_cols_max = kXStageBytes / (2 * std::max(1, M));
-  p.seg_slabs = std::max(1, std::min(sps, (seg_cols_max - 8) / slab));
-  p.workspace_bytes = splits > 1 ? (size_t)splits * per_split : 0;
+  int seg = std::max(1, std::min(sps, (seg_cols_max - 8) / slab));
+  if (L.bits == 4 && seg < sps) seg = std::max(kPF, seg / kPF * kPF);
+  p.seg_slabs = seg;
+  p.workspace_bytes = (splits > 1 || need_partials) ? (size_t)splits * per_split + hbytes : 0;
   return p;
 }
 
@@ -315,13 +750,13 @@ hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint1
   a.lut = L.lut;
   a.x = x;
   a.out = out;
-  a.partial = workspace;
   a.offsets = L.offsets;
   a.cols = L.cols;
   a.vals = L.vals;
   a.has_csr = (L.offsets && L.cols && L.vals) ? 1 : 0;
   a.B = D.B;
   a.H = D.H;
+  a.A = D.A;
   a.gamma = D.gamma;
   a.scale = D.scale;
   a.r = D.r;
@@ -339,20 +774,38 @@ hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint1
   const int slab = slab_cols(L.bits);
   a.xstride = plan.seg_slabs * slab + 8;
   a.splits = plan.splits;
+  a.row_blocks = (L.N + kRowsPerBlock - 1) / kRowsPerBlock;
+  const bool fused_h = D.r > 0 && D.H == nullptr && D.A != nullptr;
+  a.h_blocks = fused_h ? (L.K + kHCols - 1) / kHCols : 0;
+  a.direct_out = (plan.splits == 1 && !fused_h) ? 1 : 0;
+  a.partial = workspace;
+  a.hpart = fused_h ? workspace + (size_t)plan.splits * M * L.N : nullptr;
   a.x_vec = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (L.K % 8) == 0) ? 1 : 0;
-  const size_t lds = (size_t)M * a.xstride * sizeof(uint16_t);
-  const dim3 grid((L.N + kRowsPerBlock - 1) / kRowsPerBlock, plan.splits);
   const bool per_row = L.group_size <= 0 || L.ng == 1;
   const int mode = per_row ? 0 : ((L.group_size % window_cols(L.bits)) == 0 ? 1 : 2);
+  // 4-bit fast path: a 128-column slab holds 1, 2 or 4 whole groups (or the per-row LUT)
+  const bool fast = L.bits == 4 && L.K > 0 &&
+                    (per_row || L.group_size == 32 || L.group_size == 64 || L.group_size % 128 == 0);
+  const int ngs = (!per_row && L.group_size < 128) ? 128 / L.group_size : 1;
+  size_t lds = (size_t)M * a.xstride * sizeof(uint16_t);
+  lds = (lds + 15) & ~(size_t)15;
+  if (fast) lds += 64 + (size_t)kWaves * (16 * 4 * 64 + (per_row ? 16 * 32 : 16 * 4 * ngs * 32) + 16 * kOT * 4);
+  const int mt = M > 16 ? 2 : 1;
+  const size_t hred = fused_h ? (size_t)4 * mt * (kMaxFusedRank / 16) * 4 * 64 * sizeof(float) : 0;
+  lds = std::max(lds, hred);
+  const dim3 grid(a.h_blocks + a.row_blocks * plan.splits);
   hipError_t err;
-  switch (L.bits) {
-    case 1: err = launch_bits<1>(a, mode, grid, lds, stream); break;
-    case 2: err = launch_bits<2>(a, mode, grid, lds, stream); break;
-    case 3: err = launch_bits<3>(a, mode, grid, lds, stream); break;
-    default: err = launch_bits<4>(a, mode, grid, lds, stream); break;
-  }
+  if (M == 1)
+    err = launch_m<1, 1>(a, L.bits, mode, fast, ngs, grid, lds, stream);
+  else if (M <= 4)
+    err = launch_m<1, 4>(a, L.bits, mode, fast, ngs, grid, lds, stream);
+  else if (M <= 16)
+    err = launch_m<1, 16>(a, L.bits, mode, fast, ngs, grid, lds, stream);
+  else
+    err = launch_m<2, 32>(a, L.bits, mode, fast, ngs, grid, lds, stream);
   if (err != hipSuccess) return err;
-  if (plan.splits > 1) return launch_splitk_reduce(workspace, plan.splits, M, L.N, D, out, stream);
+  if (!a.direct_out)
+    return launch_finalize(workspace, plan.splits, M, L.N, D, a.hpart, a.h_blocks, out, stream);
   return hipSuccess;
 }
 

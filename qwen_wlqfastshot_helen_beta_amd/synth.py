@@ -201,6 +201,35 @@ def make_layer(N: int, K: int, bits: int = 4, group_size: int = 128, rank: int =
                       meta=dict(seed=seed, density=density, heavy_frac=heavy_frac, heavy_mult=heavy_mult))
 
 
+def merge_layers(parts) -> SynthLayer:
+    """Output-dimension merge of layers sharing K (vLLM's qkv_proj / gate_up_proj):
+    rows concatenated, CSR offsets rebased, DoRA A stacked along the rank and B
+    block-diagonal, as the plugin's loader merges shards."""
+    p0 = parts[0]
+    assert all(p.K == p0.K and p.bits == p0.bits and p.group_size == p0.group_size for p in parts)
+    offs, base = [], 0
+    for p in parts:
+        offs.append(p.offsets.astype(np.int64) + base)
+        base += p.nnz
+    N = sum(p.N for p in parts)
+    A = B = gamma = None
+    if all(p.B is not None for p in parts):
+        A = np.concatenate([p.A for p in parts], axis=0)
+        R = sum(p.rank for p in parts)
+        B = np.zeros((N, R), dtype=np.float16)
+        r0 = c0 = 0
+        for p in parts:
+            B[r0:r0 + p.N, c0:c0 + p.rank] = p.B
+            r0 += p.N
+            c0 += p.rank
+        gamma = np.concatenate([p.gamma for p in parts])
+    return SynthLayer(N=N, K=p0.K, bits=p0.bits, group_size=p0.group_size, wpr=p0.wpr,
+                      q=np.concatenate([p.q for p in parts]), lut=np.concatenate([p.lut for p in parts]),
+                      offsets=np.concatenate(offs).astype(np.int32), cols=np.concatenate([p.cols for p in parts]),
+                      vals=np.concatenate([p.vals for p in parts]), A=A, B=B, gamma=gamma,
+                      lora_scale=p0.lora_scale, meta=dict(merged=len(parts)))
+
+
 def make_activations(M: int, K: int, seed: int = 1) -> np.ndarray:
     rng = np.random.default_rng(seed)
     return rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)

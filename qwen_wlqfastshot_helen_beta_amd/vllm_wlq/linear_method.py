@@ -9,9 +9,11 @@ Same methods and layer attributes as the reference (vllm_wlq/linear_method.py:37
   (row-aligned codes, padded LUTs, chunk-CSR outliers, merged DoRA factors and
   the calibrated magnitude scale gamma) -- host conversions run in the native
   ``_C`` helpers, gamma uses the device dequantization ``_C.dequant_w0``;
-* ``apply`` runs one forward: fp16 activations, ``H = x A^T`` in fp16, then
-  ``torch.ops.wlq_fastShot.gemv`` (one row) or ``.gemm`` (several rows), cast
-  back to the caller's dtype and bias added in that dtype.
+* ``apply`` runs one forward: fp16 activations, then
+  ``torch.ops.wlq_fastShot.gemv`` (one row) or ``.gemm`` (several rows) with
+  ``lora_A`` so the DoRA ``H = fp16(x A^T)`` is computed inside the product
+  (the reference computes it with a separate F.linear), cast back to the
+  caller's dtype and bias added in that dtype.
 
 Tensor parallelism (the reference's general path, :676-935) is handled by vLLM
 sharding outside this module on multi-GPU deployments and is not part of this
@@ -429,16 +431,16 @@ class WLQLinearMethod(LinearMethodBase):
         bits = int(getattr(layer, "quant_bits", self.quant_config.bits))
         gs = int(getattr(layer, "wlq_group_size", 0))
         scale = float(getattr(layer, "lora_scale", 1.0))
+        A = layer.lora_A_f16 if has_dora else None
         if M == 1:
-            h = F.linear(x2.squeeze(0), layer.lora_A_f16).float() if has_dora else None
+            # H = fp32(fp16(x A^T)) is computed inside the product from lora_A
             torch.ops.wlq_fastShot.gemv(layer.q_packed_aligned, layer.lut_c, x2.squeeze(0), out.squeeze(0), layer.N,
                                         layer.K, bits, layer.chunk_offsets, layer.chunk_cols, layer.chunk_vals,
-                                        lora_B, h, gamma, scale, gs)
+                                        lora_B, None, gamma, scale, gs, A)
         else:
-            H = F.linear(x2, layer.lora_A_f16).float() if has_dora else None
             torch.ops.wlq_fastShot.gemm(x2, layer.q_packed_aligned, layer.lut_c, out, layer.N, layer.K, bits,
                                         layer.words_per_row, layer.chunk_offsets, layer.chunk_cols, layer.chunk_vals,
-                                        H, lora_B, gamma, scale, gs)
+                                        None, lora_B, gamma, scale, gs, A)
         y = out if orig_dtype == torch.float16 else out.to(orig_dtype)
         if bias is not None:
             y.add_(bias)

@@ -41,12 +41,18 @@ def layer_tensors(L: synth.SynthLayer):
     return L.to_torch(DEV)
 
 
-def run_product(vw, L: synth.SynthLayer, x: np.ndarray, with_dora: bool = True, with_csr: bool = True):
-    """Our HIP path through the torch ops; returns (y fp16 numpy, H fp32 numpy or None)."""
+def run_product(vw, L: synth.SynthLayer, x: np.ndarray, with_dora: bool = True, with_csr: bool = True,
+                fused_h: bool = False):
+    """Our HIP path through the torch ops; returns (y fp16 numpy, H fp32 numpy or None).
+
+    fused_h: pass lora_A instead of H so the op computes H = fp16(x A^T) itself;
+    the returned H is then the oracle's lora_h (exact sum rounded to fp16)."""
     t = layer_tensors(L)
     xt = torch.from_numpy(x).to(DEV)
     M = x.shape[0]
     dora = with_dora and L.B is not None
+    if dora and fused_h:
+        return _run_fused(L, t, xt, with_csr), O.lora_h(x, L.A)
     H = torch.nn.functional.linear(xt, t["lora_A"]).float() if dora else None
     out = torch.empty((M, L.N), dtype=torch.float16, device=DEV)
     off = t["chunk_offsets"] if with_csr else None
@@ -62,6 +68,22 @@ def run_product(vw, L: synth.SynthLayer, x: np.ndarray, with_dora: bool = True, 
                                     L.lora_scale, L.group_size)
     torch.cuda.synchronize()
     return out.cpu().numpy(), (H.cpu().numpy() if dora else None)
+
+
+def _run_fused(L, t, xt, with_csr):
+    M = xt.shape[0]
+    out = torch.empty((M, L.N), dtype=torch.float16, device=DEV)
+    off = t["chunk_offsets"] if with_csr else None
+    cols = t["chunk_cols"] if with_csr else None
+    vals = t["chunk_vals"] if with_csr else None
+    if M == 1:
+        torch.ops.wlq_fastShot.gemv(t["q_packed"], t["lut_c"], xt[0], out[0], L.N, L.K, L.bits, off, cols, vals,
+                                    t["lora_B"], None, t["dora_gamma"], L.lora_scale, L.group_size, t["lora_A"])
+    else:
+        torch.ops.wlq_fastShot.gemm(xt, t["q_packed"], t["lut_c"], out, L.N, L.K, L.bits, L.wpr, off, cols, vals,
+                                    None, t["lora_B"], t["dora_gamma"], L.lora_scale, L.group_size, t["lora_A"])
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
 
 
 def oracle_product(L: synth.SynthLayer, x: np.ndarray, H, with_csr: bool = True, round_gemm_output=False):

@@ -16,7 +16,7 @@ from qwen_wlqfastshot_helen_beta_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-GROUPS = {4: [0, 32, 128], 3: [0, 64, 128], 2: [0, 64, 128], 1: [0, 128]}
+GROUPS = {4: [0, 32, 64, 96, 128, 256], 3: [0, 64, 128], 2: [0, 64, 128], 1: [0, 128]}
 
 
 def _case(bits, gs):
@@ -117,19 +117,19 @@ def test_c_abi_matches_op(vw):
         H = torch.nn.functional.linear(x, t["lora_A"]).float()
         ref, _ = run_product(vw, L, x.cpu().numpy())
         out = torch.empty((M, L.N), dtype=torch.float16, device=DEV)
-        nbytes = lib.wlq_gemm_workspace_bytes(M, L.N, L.K, 4, torch.cuda.current_device())
+        nbytes = lib.wlq_gemm_workspace_bytes(M, L.N, L.K, 4, 0, torch.cuda.current_device())
         ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=DEV)
         stream = torch.cuda.current_stream().cuda_stream
         if M == 1:
             st = lib.wlq_gemv(t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), x.data_ptr(), out.data_ptr(),
                               t["chunk_offsets"].data_ptr(), t["chunk_cols"].data_ptr(), t["chunk_vals"].data_ptr(),
-                              t["lora_B"].data_ptr(), H.data_ptr(), t["dora_gamma"].data_ptr(), 1.0, 8, L.N, L.K, 4,
-                              128, ws.data_ptr(), ws.numel(), stream)
+                              t["lora_B"].data_ptr(), H.data_ptr(), t["dora_gamma"].data_ptr(), None, 1.0, 8, L.N,
+                              L.K, 4, 128, ws.data_ptr(), ws.numel(), stream)
         else:
             st = lib.wlq_gemm(x.data_ptr(), t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), out.data_ptr(), M, L.N,
                               L.K, 4, L.wpr, 128, t["chunk_offsets"].data_ptr(), t["chunk_cols"].data_ptr(),
                               t["chunk_vals"].data_ptr(), H.data_ptr(), t["lora_B"].data_ptr(),
-                              t["dora_gamma"].data_ptr(), 1.0, 8, ws.data_ptr(), ws.numel(), stream)
+                              t["dora_gamma"].data_ptr(), None, 1.0, 8, ws.data_ptr(), ws.numel(), stream)
         assert st == 0, lib.wlq_last_error()
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
@@ -138,10 +138,37 @@ def test_c_abi_matches_op(vw):
         st = lib.wlq_gemm(x.data_ptr(), t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), out2.data_ptr(), M, L.N,
                           L.K, 4, L.wpr, 128, t["chunk_offsets"].data_ptr(), t["chunk_cols"].data_ptr(),
                           t["chunk_vals"].data_ptr(), H.data_ptr(), t["lora_B"].data_ptr(), t["dora_gamma"].data_ptr(),
-                          1.0, 8, None, 0, stream)
+                          None, 1.0, 8, None, 0, stream)
         assert st == 0, lib.wlq_last_error()
         torch.cuda.synchronize()
         check_close(out2.cpu().numpy(), ref, what="no-workspace")
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 32, 40, 130])
+def test_fused_dora_h(vw, M):
+    """lora_A passed instead of H: the product computes H = fp16(x A^T) itself
+    (inside the decode kernel for M <= 32, with the lora_h kernel above)."""
+    for bits, gs, r in ((4, 128, 16), (4, 0, 64), (3, 64, 8), (4, 64, 96)):
+        L = synth.make_layer(N=260, K=2176, bits=bits, group_size=gs, rank=r, density=0.005, seed=M + r)
+        x = synth.make_activations(M, L.K, seed=M)
+        y, H = run_product(vw, L, x, fused_h=True)
+        check_close(y, oracle_product(L, x, H), what=f"fused M={M} bits={bits} gs={gs} r={r}")
+
+
+def test_fused_needs_workspace(vw):
+    """Computing H from lora_A without a workspace is refused with WLQ_ERR_CAPACITY."""
+    from qwen_wlqfastshot_helen_beta_amd import load_abi
+
+    lib = load_abi()
+    L = synth.make_layer(N=64, K=512, bits=4, group_size=128, rank=8, density=0.0, seed=1)
+    t = L.to_torch(DEV)
+    x = torch.from_numpy(synth.make_activations(1, L.K)).to(DEV)
+    out = torch.empty((1, L.N), dtype=torch.float16, device=DEV)
+    st = lib.wlq_gemv(t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), x.data_ptr(), out.data_ptr(), None, None, None,
+                      t["lora_B"].data_ptr(), None, t["dora_gamma"].data_ptr(), t["lora_A"].data_ptr(), 1.0, 8, L.N,
+                      L.K, 4, 128, None, 0, torch.cuda.current_stream().cuda_stream)
+    assert st == 4, st
+    assert b"workspace" in lib.wlq_last_error()
 
 
 def test_dora_epilogue_entry(vw):
