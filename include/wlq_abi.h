@@ -31,12 +31,16 @@
  * multiple of 32 columns, at least the code window (32/40/64/128 columns for
  * 4/3/2/1 bits) and below 4096; a group_size >= K is the per-row case.
  *
- * Workspace: split-K partial sums (fp32) and, when H is computed from
- * lora_A, its partial sums.  Pass the buffer and its size; when it is smaller
- * than wlq_gemm_workspace_bytes() the split count is reduced to what fits.  No
- * workspace is valid unless H has to be computed from lora_A (then
- * WLQ_ERR_CAPACITY reports the minimum).  Calls that share one workspace must
- * be ordered on one stream.
+ * Workspace: its first 16 KiB hold arrival counters (the block of the decode
+ * kernel that finishes last for a group of 64 output rows applies the
+ * epilogue, so no second kernel is needed); the rest holds split-K partial sums
+ * (fp32) and, when H is computed from lora_A, its partial sums.  ZERO-FILL A
+ * WORKSPACE ONCE AFTER ALLOCATING IT (e.g. hipMemset): the counters must start
+ * at zero, and every call leaves them zero again.  Pass the buffer and its
+ * size; when it is smaller than wlq_gemm_workspace_bytes() the split count is
+ * reduced to what fits.  No workspace is valid unless H has to be computed
+ * from lora_A (then WLQ_ERR_CAPACITY reports the minimum).  Calls that share
+ * one workspace must be ordered on one stream.
  */
 #ifndef WLQ_ABI_H
 #define WLQ_ABI_H
@@ -50,7 +54,7 @@
 extern "C" {
 #endif
 
-#define WLQ_ABI_VERSION 2
+#define WLQ_ABI_VERSION 3
 
 enum wlq_status {
   WLQ_OK = 0,

@@ -79,7 +79,8 @@ torch::Tensor workspace_for(const torch::Device& dev, size_t bytes) {
   std::lock_guard<std::mutex> lk(g_ws_mu);
   auto& t = g_ws[dev.index()];
   if (!t.defined() || (size_t)t.numel() < bytes) {
-    t = torch::empty({(int64_t)std::max<size_t>(bytes, 256)}, torch::TensorOptions().dtype(torch::kUInt8).device(dev));
+    // zero-filled: the leading arrival counters must start at zero (calls leave them zero)
+    t = torch::zeros({(int64_t)std::max<size_t>(bytes, 256)}, torch::TensorOptions().dtype(torch::kUInt8).device(dev));
   }
   return t;
 }

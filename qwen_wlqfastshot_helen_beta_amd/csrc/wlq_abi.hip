@@ -144,6 +144,14 @@ int run_product(const wlq::Layer& L, wlq::Dora D, const void* X, void* out, int6
   const int cus = current_cu_count();
   size_t ws = workspace != nullptr ? workspace_bytes : 0;
   char* wbase = reinterpret_cast<char*>(workspace);
+  uint32_t* sync = nullptr;  // arrival counters at the front of the workspace
+  if (ws >= wlq::kSyncBytes) {
+    sync = reinterpret_cast<uint32_t*>(wbase);
+    wbase += wlq::kSyncBytes;
+    ws -= wlq::kSyncBytes;
+  } else {
+    ws = 0;
+  }
   const uint16_t* x = reinterpret_cast<const uint16_t*>(X);
   uint16_t* y = reinterpret_cast<uint16_t*>(out);
   const bool skinny = M <= wlq::skinny_max_m();
@@ -171,7 +179,7 @@ int run_product(const wlq::Layer& L, wlq::Dora D, const void* X, void* out, int6
                      p.workspace_bytes, ws);
       return WLQ_ERR_CAPACITY;
     }
-    return hip_status(wlq::launch_skinny(L, D, x, y, (int)M, p, w, stream), fn);
+    return hip_status(wlq::launch_skinny(L, D, x, y, (int)M, p, w, sync, stream), fn);
   }
   const wlq::SplitPlan p = wlq::plan_gemm(L, (int)M, cus, ws);
   return hip_status(wlq::launch_gemm(L, D, x, y, (int)M, p, w, stream), fn);
@@ -197,7 +205,8 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
   const size_t hb = (r > 0 && !fused) ? round_up((size_t)M * r * sizeof(float)) : 0;
   const wlq::SplitPlan p = skinny ? wlq::plan_skinny(L, (int)M, cus, unlimited, fused ? r : 0)
                                   : wlq::plan_gemm(L, (int)M, cus, unlimited);
-  return hb + p.workspace_bytes;
+  const size_t need = hb + p.workspace_bytes;
+  return need > 0 ? wlq::kSyncBytes + need : 0;
 }
 
 int wlq_gemv(const int32_t* q_packed, const void* lut_c, const void* x, void* out, const int32_t* chunk_offsets,

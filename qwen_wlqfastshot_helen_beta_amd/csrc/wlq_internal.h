@@ -38,13 +38,21 @@ struct SplitPlan {
   size_t workspace_bytes;   // fp32 partials needed (0 when splits == 1)
 };
 
+// The first kSyncBytes of a caller's workspace hold arrival counters of the decode
+// kernel (one 32-bit word per 64-row block).  They must be zero before the first call
+// on a workspace and every call leaves them zero.  Products, H and partials use the
+// bytes after them.
+constexpr size_t kSyncBytes = 16384;
+constexpr int kMaxSyncRowBlocks = (int)(kSyncBytes / 4);
+
 int slab_cols(int bits);             // columns one 16-row wave tile covers per step
 int skinny_max_m();
 int skinny_max_fused_rank();         // largest DoRA rank whose H the decode kernel computes itself
 // fused_rank > 0: H will be computed from lora_A inside the decode product.
 SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_bytes, int fused_rank);
+// sync: the workspace's arrival counters, or nullptr (a finalize kernel then finishes).
 hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint16_t* out, int M,
-                         const SplitPlan& plan, float* workspace, hipStream_t stream);
+                         const SplitPlan& plan, float* workspace, uint32_t* sync, hipStream_t stream);
 
 SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes);
 hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_t* out, int M,

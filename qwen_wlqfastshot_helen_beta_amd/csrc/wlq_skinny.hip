@@ -53,6 +53,7 @@ constexpr int kMaxSplits = 64;
 constexpr int kPF = 4;               // slabs in flight per wave (4-bit path)
 constexpr int kHCols = 512;          // columns per DoRA block
 constexpr int kMaxFusedRank = 64;
+constexpr int kMaxFastSlabs = 60;    // slabs per 4-bit block: any start slab then spans <= 16 chunks
 
 struct SkinnyArgs {
   const uint32_t* q;
@@ -76,7 +77,26 @@ struct SkinnyArgs {
   int x_vec;         // 16-byte loads of x rows are aligned
   int has_csr;
   int direct_out;    // epilogue in this kernel (one split, H given)
+  // In-kernel completion: arrival counters (one per row block, zero between calls);
+  // the block that arrives last for a row block sums the partials and applies the
+  // epilogue.  Arrivals per row block = splits + h_blocks.
+  uint32_t* sync;    // nullptr: a separate finalize kernel finishes
+  int arrivals;
 };
+
+// Cross-block hand-off without cache maintenance: partials and DoRA partials are
+// stored and loaded as device-scope (relaxed) atomics, which are coherent across
+// the XCDs' L2 caches; a block waits for its stores to complete before it counts
+// its arrival, and the last block loads only after its count returned.  (Full
+// device-scope fences would write back / invalidate whole L2 caches instead.)
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void fence_release() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void fence_acquire() { asm volatile("" ::: "memory"); }
 
 __device__ __forceinline__ int group_of(int col, uint32_t magic) { return (int)__umulhi((uint32_t)col, magic); }
 
@@ -124,7 +144,7 @@ __device__ __forceinline__ u32x4_t load8(const uint16_t* row, int k, int K, bool
 // for i < M, j < r, with MFMA 16x16x32 (both operands in natural k order).
 // Wave w covers 128 columns; the four wave partials are summed through LDS.
 template <int MT>
-__device__ void dora_h_block(const SkinnyArgs& a, int hb, float* red) {
+__device__ __forceinline__ void dora_h_block(const SkinnyArgs& a, int hb, float* red) {
   constexpr int JT = kMaxFusedRank / 16;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -178,7 +198,7 @@ __device__ void dora_h_block(const SkinnyArgs& a, int hb, float* red) {
     const int mt = t / JT;
     const int i = 16 * mt + 4 * (ln >> 4) + e;
     const int j = 16 * jt + (ln & 15);
-    if (i < a.M && j < a.r) a.hpart[((size_t)hb * a.M + i) * a.r + j] = v;
+    if (i < a.M && j < a.r) store_dev(a.hpart + ((size_t)hb * a.M + i) * a.r + j, v);
   }
 }
 
@@ -243,10 +263,110 @@ __device__ __forceinline__ void write_result(const SkinnyArgs& a, int split, int
           }
           a.out[(size_t)i * a.N + n] = f2h_rn(v);
         } else {
-          a.partial[((size_t)split * a.M + i) * a.N + n] = v;
+          store_dev(a.partial + ((size_t)split * a.M + i) * a.N + n, v);
         }
       }
     }
+  }
+}
+
+
+// Sum of n_terms device-scope loads p[0], p[stride], ... in index order; the loads
+// are issued eight at a time so their latencies overlap.
+__device__ __forceinline__ float sum_dev(const float* p, size_t stride, int n_terms) {
+  float v = 0.f;
+  for (int t0 = 0; t0 < n_terms; t0 += 8) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) t[u] = load_dev(p + (size_t)min(t0 + u, n_terms - 1) * stride);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (t0 + u < n_terms) v += t[u];
+  }
+  return v;
+}
+
+// Epilogue for the row blocks rbs[0..count) (rb0 when rbs is null), run by the block that arrived last on
+// each of them: y[i, n] = fp16_rn((sum_s partial[s, i, n] + scale * h[i, :] . B[n, :]) * gamma[n])
+// with h = fp16(sum over DoRA blocks of hpart) (or the caller's H).  Splits and DoRA
+// blocks are summed in index order, so the result does not depend on arrival order.
+// lds: at least M * r free floats.
+__device__ __forceinline__ void finish_rows(const SkinnyArgs& a, int rb0, const int* rbs, int count, float* lds) {
+  const float* h = a.H;
+  if (a.r > 0 && a.hpart != nullptr) {
+    for (int idx = threadIdx.x; idx < a.M * a.r; idx += blockDim.x)
+      lds[idx] = h2f(f2h_rn(sum_dev(a.hpart + idx, (size_t)a.M * a.r, a.h_blocks)));
+    __syncthreads();
+    h = lds;
+  }
+  const size_t plane = (size_t)a.M * a.N;
+  const bool bvec = (a.r & 7) == 0 && (reinterpret_cast<uintptr_t>(a.B) & 15u) == 0;
+  for (int t = threadIdx.x; t < count * a.M * kRowsPerBlock; t += blockDim.x) {
+    const int k = t / (a.M * kRowsPerBlock);
+    const int u = t - k * (a.M * kRowsPerBlock);
+    const int i = u / kRowsPerBlock;
+    const int n = (rbs ? rbs[k] : rb0) * kRowsPerBlock + (u - i * kRowsPerBlock);
+    if (n >= a.N) continue;
+    const size_t idx = (size_t)i * a.N + n;
+    float v = sum_dev(a.partial + idx, plane, a.splits);
+    if (a.r > 0) {
+      float ls = 0.f;
+      const float* hi = h + (size_t)i * a.r;
+      const uint16_t* b = a.B + (size_t)n * a.r;
+      if (bvec) {
+        for (int j = 0; j < a.r; j += 8) {
+          const u32x4_t bv = *reinterpret_cast<const u32x4_t*>(b + j);
+          const uint32_t w[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            ls += hi[j + 2 * q] * h2f((uint16_t)(w[q] & 0xFFFFu));
+            ls += hi[j + 2 * q + 1] * h2f((uint16_t)(w[q] >> 16));
+          }
+        }
+      } else {
+        for (int j = 0; j < a.r; ++j) ls += hi[j] * h2f(b[j]);
+      }
+      v = (v + a.scale * ls) * h2f(a.gamma[n]);
+    }
+    a.out[idx] = f2h_rn(v);
+  }
+}
+
+// Product block: partials are written; count the arrival and finish the row block
+// when this block is the last one.
+__device__ __forceinline__ void arrive_product(const SkinnyArgs& a, int rb, float* lds) {
+  __shared__ int s_last;
+  fence_release();  // this block's partial stores are complete before it counts
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(a.sync + rb, 1u) == (uint32_t)(a.arrivals - 1);
+  __syncthreads();
+  if (!s_last) return;
+  fence_acquire();
+  finish_rows(a, rb, nullptr, 1, lds);
+  if (threadIdx.x == 0) atomicExch(a.sync + rb, 0u);  // ready for the next call
+}
+
+// DoRA block: hpart is written; count one arrival on every row block and finish,
+// in one parallel pass, the row blocks for which this block is the last.
+__device__ __forceinline__ void arrive_dora(const SkinnyArgs& a, float* lds) {
+  __shared__ int s_list[256];
+  __shared__ int s_n;
+  fence_release();
+  for (int base = 0; base < a.row_blocks; base += blockDim.x) {
+    if (threadIdx.x == 0) s_n = 0;
+    __syncthreads();
+    const int rb = base + (int)threadIdx.x;
+    if (rb < a.row_blocks && atomicAdd(a.sync + rb, 1u) == (uint32_t)(a.arrivals - 1))
+      s_list[atomicAdd(&s_n, 1)] = rb;
+    __syncthreads();
+    const int cnt = s_n;
+    if (cnt > 0) {
+      fence_acquire();
+      finish_rows(a, 0, s_list, cnt, lds);
+      __syncthreads();
+      if ((int)threadIdx.x < cnt) atomicExch(a.sync + s_list[threadIdx.x], 0u);
+    }
+    __syncthreads();
   }
 }
 
@@ -303,6 +423,10 @@ __global__ __launch_bounds__(256) void skinny_generic_kernel(const SkinnyArgs a)
   int bid = blockIdx.x;
   if (bid < a.h_blocks) {
     dora_h_block<MT>(a, bid, reinterpret_cast<float*>(xs));
+    if (a.sync) {
+      __syncthreads();
+      arrive_dora(a, reinterpret_cast<float*>(xs));
+    }
     return;
   }
   bid -= a.h_blocks;
@@ -371,9 +495,59 @@ __global__ __launch_bounds__(256) void skinny_generic_kernel(const SkinnyArgs a)
   if (a.has_csr)
     outlier_delta<BITS, MT, MB, PER_ROW>(a, n, row_ok, kq, t_begin * SLAB, min(a.K, t_end * SLAB), qrow, lrow, acc);
   write_result<MT>(a, split, n, row_ok, kq, acc);
+  if (a.sync) {
+    __syncthreads();  // the activation tile is free from here on
+    arrive_product(a, rb, reinterpret_cast<float*>(xs));
+  }
 }
 
 // -------------------------------------------------------------- 4-bit fast path
+
+// Activation staging in two phases (fast path, 16-byte aligned rows, K % 8 == 0):
+// xstage_load issues the loads of the first kXR 8-column units per thread (unit
+// indices clamped, so the loads are unconditional), xstage_store writes them to LDS
+// in order P and stages any remaining units directly.
+constexpr int kXR = 4;
+struct XStage {
+  u32x4_t v[kXR];
+};
+
+__device__ __forceinline__ void xstage_load(const SkinnyArgs& a, XStage& xr, int c_a, int ncols) {
+  const int upr = ncols >> 3;
+  const int total = a.M * upr;
+#pragma unroll
+  for (int k = 0; k < kXR; ++k) {
+    const int u = min((int)threadIdx.x + k * (int)blockDim.x, max(total - 1, 0));
+    const int i = u / upr;
+    const int col = min(c_a + ((u - i * upr) << 3), a.K - 8);
+    xr.v[k] = *reinterpret_cast<const u32x4_t*>(a.x + (size_t)i * a.K + col);
+  }
+}
+
+__device__ __forceinline__ void xstage_store(const SkinnyArgs& a, const XStage& xr, uint16_t* xs, int c_a,
+                                             int ncols) {
+  const int upr = ncols >> 3;
+  const int total = a.M * upr;
+#pragma unroll
+  for (int k = 0; k < kXR; ++k) {
+    const int u = (int)threadIdx.x + k * (int)blockDim.x;
+    if (u < total) {
+      const int i = u / upr;
+      const int c8 = u - i * upr;
+      const bool inside = c_a + (c8 << 3) < a.K;  // K % 8 == 0: a unit is all inside or all outside
+      const u32x4_t v = inside ? permute_p(xr.v[k]) : u32x4_t{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4_t*>(xs + i * a.xstride + (c8 << 3)) = v;
+    }
+  }
+  for (int u = (int)threadIdx.x + kXR * (int)blockDim.x; u < total; u += blockDim.x) {
+    const int i = u / upr;
+    const int c8 = u - i * upr;
+    const int col = c_a + (c8 << 3);
+    const u32x4_t v = col < a.K ? permute_p(*reinterpret_cast<const u32x4_t*>(a.x + (size_t)i * a.K + col))
+                                : u32x4_t{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4_t*>(xs + i * a.xstride + (c8 << 3)) = v;
+  }
+}
 
 constexpr int kEB = 4;  // CSR entries per lane fetched ahead for the next chunk
 
@@ -417,8 +591,10 @@ __device__ __forceinline__ void fast_block(const u32x4_t& codes, const LutPlanes
 }
 
 // Wave-private LDS tiles of one outlier chunk (4 slabs x 16 rows):
-//   ctile: code windows, [row][slab][kq] x 16 B
-//   ltile: LUT byte planes (lo 16 B | hi 16 B), [row][slab][group] x 32 B
+//   ctile: code windows, [slab][kq][row] x 16 B
+//   ltile: LUT byte planes, [slab][group][lo|hi][row] x 16 B (the per-row LUT: [lo|hi][row])
+// Rows are the fastest index, so the 64 lanes of a wave write 64 consecutive words
+// or 16-byte chunks: no LDS bank conflicts on the per-slab stores and reads.
 template <int NGS>
 struct ChunkTiles {
   uint32_t* ctile;
@@ -429,19 +605,19 @@ template <bool PER_ROW, int NGS, int MT>
 __device__ __forceinline__ void stage4_consume(const Stage4<NGS>& s, int slab_in_chunk, LutPlanes<4>& pl,
                                                const ChunkTiles<NGS>& tl, int r, int kq,
                                                const uint16_t* const xp[MT], float4_t acc[MT]) {
-  *reinterpret_cast<u32x4_t*>(tl.ctile + ((r * 4 + slab_in_chunk) * 4 + kq) * 4) = s.codes;
+  *reinterpret_cast<u32x4_t*>(tl.ctile + ((slab_in_chunk * 4 + kq) * 16 + r) * 4) = s.codes;
   if constexpr (!PER_ROW) {
     // split my LUT quarters into planes and exchange them with the row's other lanes
 #pragma unroll
     for (int j = 0; j < NGS; ++j) {
-      uint32_t* base = tl.ltile + ((r * 4 + slab_in_chunk) * NGS + j) * 8;
-      base[kq] = perm_b32(s.lq[j].y, s.lq[j].x, 0x06040200u);
-      base[4 + kq] = perm_b32(s.lq[j].y, s.lq[j].x, 0x07050301u);
+      uint32_t* base = tl.ltile + ((slab_in_chunk * NGS + j) * 2 * 16 + r) * 4 + kq;
+      base[0] = perm_b32(s.lq[j].y, s.lq[j].x, 0x06040200u);
+      base[16 * 4] = perm_b32(s.lq[j].y, s.lq[j].x, 0x07050301u);
     }
     const int jown = (NGS == 1) ? 0 : (NGS == 2 ? (kq >> 1) : kq);
-    const uint32_t* own = tl.ltile + ((r * 4 + slab_in_chunk) * NGS + jown) * 8;
+    const uint32_t* own = tl.ltile + ((slab_in_chunk * NGS + jown) * 2 * 16 + r) * 4;
     const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(own);
-    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(own + 4);
+    const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(own + 16 * 4);
     pl.lo[0] = lo.x; pl.lo[1] = lo.y; pl.lo[2] = lo.z; pl.lo[3] = lo.w;
     pl.hi[0] = hi.x; pl.hi[1] = hi.y; pl.hi[2] = hi.z; pl.hi[3] = hi.w;
   }
@@ -484,12 +660,12 @@ __device__ __forceinline__ void entry_delta(const SkinnyArgs& a, const ChunkTile
   const int gcol = c * 512 + cl;
   if (gcol < k_lo || gcol >= k_hi) return;
   const int sl = cl >> 7;
-  const uint32_t word = tl.ctile[((r * 4 + sl) * 4 + ((cl >> 5) & 3)) * 4 + ((cl >> 3) & 3)];
+  const uint32_t word = tl.ctile[((sl * 4 + ((cl >> 5) & 3)) * 16 + r) * 4 + ((cl >> 3) & 3)];
   const uint32_t code = (word >> (4 * (cl & 7))) & 15u;
   const int gi = PER_ROW ? 0 : (NGS == 1 ? 0 : (NGS == 2 ? ((cl >> 6) & 1) : ((cl >> 5) & 3)));
   const unsigned char* planes =
-      reinterpret_cast<const unsigned char*>(tl.ltile + (PER_ROW ? r * 8 : ((r * 4 + sl) * NGS + gi) * 8));
-  const uint32_t lutv = (uint32_t)planes[code] | ((uint32_t)planes[16 + code] << 8);
+      reinterpret_cast<const unsigned char*>(tl.ltile + ((PER_ROW ? 0 : (sl * NGS + gi) * 2 * 16) + r) * 4);
+  const uint32_t lutv = (uint32_t)planes[code] | ((uint32_t)planes[16 * 16 + code] << 8);
   const float d = h2f((uint16_t)(vb << 8)) - h2f((uint16_t)lutv);
   const int xc = gcol - x_col0;  // column inside the staged activation segment
   const int xi = (xc & ~7) + p_slot(xc & 7);
@@ -514,10 +690,10 @@ __device__ __forceinline__ void chunk_outliers(const SkinnyArgs& a, const ChunkE
     entry_delta<MB, PER_ROW, NGS>(a, tl, xs, r, c, (int)a.cols[e], (uint32_t)a.vals[e], k_lo, k_hi, x_col0, corr);
 }
 
-constexpr int kOT = 17;  // chunk offsets per row kept in LDS (16 chunks = 64 slabs per block)
+constexpr int kOT = 17;  // chunk offsets per row kept in LDS (a block spans at most 16 chunks)
 
 template <int MT, int MB, bool PER_ROW, int NGS>
-__global__ __launch_bounds__(256) void skinny4_kernel(const SkinnyArgs a) {
+__global__ __launch_bounds__(256, (NGS >= 4 || MT > 1 || (MB > 4 && NGS > 1)) ? 2 : 3) void skinny4_kernel(const SkinnyArgs a) {
   constexpr int SLAB = 128;
   extern __shared__ __align__(16) uint16_t smem[];
   // LDS: [x staging: M * xstride halves][64 B zeros]
@@ -527,6 +703,10 @@ __global__ __launch_bounds__(256) void skinny4_kernel(const SkinnyArgs a) {
   int bid = blockIdx.x;
   if (bid < a.h_blocks) {
     dora_h_block<MT>(a, bid, reinterpret_cast<float*>(smem));
+    if (a.sync) {
+      __syncthreads();
+      arrive_dora(a, reinterpret_cast<float*>(smem));
+    }
     return;
   }
   bid -= a.h_blocks;
@@ -552,13 +732,16 @@ __global__ __launch_bounds__(256) void skinny4_kernel(const SkinnyArgs a) {
   int* otile = reinterpret_cast<int*>(wave_lds + 16 * 4 * 4 * 4 + kLtWords) + r * kOT;
 
   const int total_slabs = (a.K + SLAB - 1) / SLAB;
-  const int t_begin = split * a.slabs_per_split;  // a multiple of 4 (chunk aligned)
+  const int t_begin = split * a.slabs_per_split;  // any slab: the first chunk may be partial
   const int t_end = min(total_slabs, t_begin + a.slabs_per_split);
   const int k_lo = t_begin * SLAB;
   const int k_hi = min(a.K, t_end * SLAB);
   const int c_begin = t_begin >> 2;
   const int c_end = (t_end + 3) >> 2;
   const int nchunks = c_end - c_begin;  // <= kOT - 1 (the planner bounds the split)
+  const bool single = a.seg_slabs >= a.slabs_per_split;
+  int seg0 = t_begin;
+  int seg_end = single ? t_end : min(t_end, (c_begin + a.seg_slabs / 4) * 4);  // segments end on chunks
 
   float4_t acc[MT];
 #pragma unroll
@@ -568,36 +751,46 @@ __global__ __launch_bounds__(256) void skinny4_kernel(const SkinnyArgs a) {
   for (int i = 0; i < MB; ++i) corr[i] = 0.f;
   const bool csr = a.has_csr != 0 && t_begin < t_end;
 
+  // Prologue.  Small loads first (CSR offsets, activations, the per-row LUT), then the
+  // code prefetch, then the LDS stores: the stores wait only for the small loads, so
+  // the first code windows are in flight while the block stages its tiles.
+  int offv[(kOT + 3) / 4];
+  {  // without outliers the loads read word 0 of the codes and the values are dropped
+    const int32_t* offr = csr ? a.offsets + (size_t)nc * (a.nch + 1) + c_begin : reinterpret_cast<const int32_t*>(a.q);
+#pragma unroll
+    for (int jj = 0; jj < (kOT + 3) / 4; ++jj) {
+      const int v = offr[csr ? min(kq + 4 * jj, nchunks) : 0];
+      offv[jj] = csr ? v : 0;
+    }
+  }
+  XStage xr;
+  const bool xfast = a.x_vec != 0;
+  if (xfast) xstage_load(a, xr, seg0 * SLAB, (seg_end - seg0) * SLAB);
+  LutRaw<4> raw;
+  if constexpr (PER_ROW) lut_load<4>(raw, lrow);
+  Stage4<NGS> st[4];  // slot s holds slab 4c + s of chunk c
+  const int t_last = max(t_end - 1, t_begin);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    stage4_load<PER_ROW, NGS>(st[j], a, qrow, lrow, kq, min(max(4 * c_begin + j, t_begin), t_last));
+#pragma unroll
+  for (int jj = 0; jj < (kOT + 3) / 4; ++jj) otile[min(kq + 4 * jj, nchunks)] = offv[jj];
+  if (xfast)
+    xstage_store(a, xr, xs, seg0 * SLAB, (seg_end - seg0) * SLAB);
+  else
+    stage_x(a, xs, seg0 * SLAB, (seg_end - seg0) * SLAB);
   LutPlanes<4> pl;
   if constexpr (PER_ROW) {
-    LutRaw<4> raw;
-    lut_load<4>(raw, lrow);
     pl = lut_planes<4>(raw);
     if (kq == 0) {
 #pragma unroll
       for (int p = 0; p < 4; ++p) {
-        tl.ltile[r * 8 + p] = pl.lo[p];
-        tl.ltile[r * 8 + 4 + p] = pl.hi[p];
+        tl.ltile[r * 4 + p] = pl.lo[p];
+        tl.ltile[(16 + r) * 4 + p] = pl.hi[p];
       }
     }
   }
   if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zpad)[threadIdx.x] = 0u;
-  // the row's chunk offsets for the block's range, once (all zero without outliers)
-  if (csr) {
-    const int32_t* offr = a.offsets + (size_t)nc * (a.nch + 1) + c_begin;
-    for (int j = kq; j <= nchunks; j += 4) otile[j] = offr[j];
-  } else {
-    for (int j = kq; j <= nchunks; j += 4) otile[j] = 0;
-  }
-
-  // prologue: codes of the first chunk, activations, entries of the first chunk
-  Stage4<NGS> st[4];
-  const int t_last = max(t_end - 1, t_begin);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) stage4_load<PER_ROW, NGS>(st[j], a, qrow, lrow, kq, min(t_begin + j, t_last));
-  int seg0 = t_begin;
-  int seg_end = min(t_end, t_begin + a.seg_slabs);
-  stage_x(a, xs, seg0 * SLAB, (seg_end - seg0) * SLAB);
   __syncthreads();
   // A row with entries in the range reads only entries below its last offset; a row
   // without any reads word 0 of its codes instead (the CSR arrays may then be empty).
@@ -607,35 +800,46 @@ __global__ __launch_bounds__(256) void skinny4_kernel(const SkinnyArgs a) {
   ChunkEntries ea, eb;
   entries_load(ea, colp, valp, kq, otile[0], otile[min(1, nchunks)]);
 
-  // one chunk: entries of the next chunk are requested, the four slabs consumed (each
-  // slab's codes re-requested four slabs ahead), then this chunk's outliers applied
-  auto chunk = [&](int c, const ChunkEntries& cur, ChunkEntries& nxt) {
+  // One chunk: the entries of the next chunk are requested, the chunk's slabs consumed
+  // (each slot re-requested for the next chunk), then the chunk's outliers applied.
+  // The last chunk requests nothing, so no load is left in flight at the end.
+  auto chunk = [&](int c, const ChunkEntries& cur, ChunkEntries& nxt, auto more) __attribute__((always_inline)) {
+    constexpr bool kMore = decltype(more)::value;
     const int lc = c - c_begin;
-    entries_load(nxt, colp, valp, kq, otile[min(lc + 1, nchunks)], otile[min(lc + 2, nchunks)]);
-    const int t0 = 4 * c;
+    if constexpr (kMore)
+      entries_load(nxt, colp, valp, kq, otile[min(lc + 1, nchunks)], otile[min(lc + 2, nchunks)]);
     const uint16_t* xp[MT];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int t = t0 + s;
-      if (t < t_end) {
+      const int t = 4 * c + s;
+      if (t >= t_begin && t < t_end) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           xp[mt] = (16 * mt + r < a.M) ? xs + (16 * mt + r) * a.xstride + (t - seg0) * SLAB + kq * 32 : zpad;
         stage4_consume<PER_ROW, NGS, MT>(st[s], s, pl, tl, r, kq, xp, acc);
       }
-      stage4_load<PER_ROW, NGS>(st[s], a, qrow, lrow, kq, min(t + 4, t_last));
+      if constexpr (kMore) stage4_load<PER_ROW, NGS>(st[s], a, qrow, lrow, kq, min(t + 4, t_last));
     }
     if (csr && row_ok) chunk_outliers<MB, PER_ROW, NGS>(a, cur, tl, xs, r, kq, c, k_lo, k_hi, seg0 * SLAB, corr);
   };
+  using More = std::integral_constant<bool, true>;
+  using Last = std::integral_constant<bool, false>;
 
-  if (a.seg_slabs >= a.slabs_per_split) {
-    for (int c = c_begin; c < c_end; c += 2) {  // two chunks per trip: the entry registers alternate
-      chunk(c, ea, eb);
-      if (c + 1 < c_end) chunk(c + 1, eb, ea);
+  if (single) {
+    int c = c_begin;
+    for (; c + 2 < c_end; c += 2) {  // two chunks per trip: the entry registers alternate
+      chunk(c, ea, eb, More{});
+      chunk(c + 1, eb, ea, More{});
+    }
+    if (c + 1 < c_end) {
+      chunk(c, ea, eb, More{});
+      chunk(c + 1, eb, ea, Last{});
+    } else {
+      chunk(c, ea, eb, Last{});
     }
   } else {
-    auto restage = [&](int c) {
-      if (4 * c >= seg_end) {  // next activation segment (segments are whole chunks)
+    auto restage = [&](int c) __attribute__((always_inline)) {
+      if (4 * c >= seg_end) {  // next activation segment (whole chunks)
         __syncthreads();
         seg0 = 4 * c;
         seg_end = min(t_end, seg0 + a.seg_slabs);
@@ -643,13 +847,21 @@ __global__ __launch_bounds__(256) void skinny4_kernel(const SkinnyArgs a) {
         __syncthreads();
       }
     };
-    for (int c = c_begin; c < c_end; c += 2) {
+    int c = c_begin;
+    for (; c + 2 < c_end; c += 2) {
       restage(c);
-      chunk(c, ea, eb);
-      if (c + 1 < c_end) {
-        restage(c + 1);
-        chunk(c + 1, eb, ea);
-      }
+      chunk(c, ea, eb, More{});
+      restage(c + 1);
+      chunk(c + 1, eb, ea, More{});
+    }
+    if (c + 1 < c_end) {
+      restage(c);
+      chunk(c, ea, eb, More{});
+      restage(c + 1);
+      chunk(c + 1, eb, ea, Last{});
+    } else {
+      restage(c);
+      chunk(c, ea, eb, Last{});
     }
   }
 
@@ -665,6 +877,10 @@ __global__ __launch_bounds__(256) void skinny4_kernel(const SkinnyArgs a) {
     }
   }
   write_result<MT>(a, split, n, row_ok, kq, acc);
+  if (a.sync) {
+    __syncthreads();
+    arrive_product(a, rb, reinterpret_cast<float*>(smem));
+  }
 }
 
 // ------------------------------------------------------------------- dispatch
@@ -718,7 +934,7 @@ SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_byte
   const int slab = slab_cols(L.bits);
   const int total = std::max(1, (L.K + slab - 1) / slab);
   const int row_blocks = (L.N + kRowsPerBlock - 1) / kRowsPerBlock;
-  const int target = 2 * std::max(1, cu_count);
+  const int target = 2 * std::max(1, cu_count);  // two blocks per CU (measured flat from 2 to 6)
   int splits = std::max(1, (target + row_blocks - 1) / row_blocks);
   splits = std::min(splits, std::min(total, kMaxSplits));
   const size_t per_split = (size_t)M * (size_t)L.N * sizeof(float);
@@ -726,11 +942,13 @@ SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_byte
   const bool need_partials = fused_rank > 0;  // the fused DoRA path always finishes in finalize
   while (splits > 1 && (size_t)splits * per_split + hbytes > workspace_bytes) --splits;
   int sps = (total + splits - 1) / splits;
-  const int spc = std::max(1, L.chunk / slab);
-  if (sps >= spc) sps = (sps + spc - 1) / spc * spc;
-  if (L.bits == 4) {  // whole outlier chunks, at most 16 per block (their offsets are staged in LDS)
-    sps = std::max(kPF, (sps + kPF - 1) / kPF * kPF);
-    sps = std::min(sps, 64);
+  if (L.bits == 4) {
+    // fast path: whole outlier chunks per block (a partial first chunk is supported but
+    // measured slower), at most 16 chunks (their offsets are staged in LDS)
+    sps = std::min(std::max(kPF, (sps + kPF - 1) / kPF * kPF), kMaxFastSlabs / kPF * kPF);
+  } else {
+    const int spc = std::max(1, L.chunk / slab);
+    if (sps >= spc) sps = (sps + spc - 1) / spc * spc;
   }
   splits = (total + sps - 1) / sps;
   p.splits = splits;
@@ -744,7 +962,7 @@ SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_byte
 }
 
 hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint16_t* out, int M,
-                         const SplitPlan& plan, float* workspace, hipStream_t stream) {
+                         const SplitPlan& plan, float* workspace, uint32_t* sync, hipStream_t stream) {
   SkinnyArgs a{};
   a.q = L.q;
   a.lut = L.lut;
@@ -778,6 +996,9 @@ hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint1
   const bool fused_h = D.r > 0 && D.H == nullptr && D.A != nullptr;
   a.h_blocks = fused_h ? (L.K + kHCols - 1) / kHCols : 0;
   a.direct_out = (plan.splits == 1 && !fused_h) ? 1 : 0;
+  const bool inline_fin = !a.direct_out && sync != nullptr && a.row_blocks <= kMaxSyncRowBlocks;
+  a.sync = inline_fin ? sync : nullptr;
+  a.arrivals = plan.splits + a.h_blocks;
   a.partial = workspace;
   a.hpart = fused_h ? workspace + (size_t)plan.splits * M * L.N : nullptr;
   a.x_vec = ((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (L.K % 8) == 0) ? 1 : 0;
@@ -793,6 +1014,7 @@ hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint1
   const int mt = M > 16 ? 2 : 1;
   const size_t hred = fused_h ? (size_t)4 * mt * (kMaxFusedRank / 16) * 4 * 64 * sizeof(float) : 0;
   lds = std::max(lds, hred);
+  if (inline_fin && D.r > 0) lds = std::max(lds, (size_t)M * D.r * sizeof(float));  // rounded H
   const dim3 grid(a.h_blocks + a.row_blocks * plan.splits);
   hipError_t err;
   if (M == 1)
@@ -804,7 +1026,7 @@ hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint1
   else
     err = launch_m<2, 32>(a, L.bits, mode, fast, ngs, grid, lds, stream);
   if (err != hipSuccess) return err;
-  if (!a.direct_out)
+  if (!a.direct_out && !inline_fin)
     return launch_finalize(workspace, plan.splits, M, L.N, D, a.hpart, a.h_blocks, out, stream);
   return hipSuccess;
 }

@@ -118,21 +118,42 @@ def test_c_abi_matches_op(vw):
         ref, _ = run_product(vw, L, x.cpu().numpy())
         out = torch.empty((M, L.N), dtype=torch.float16, device=DEV)
         nbytes = lib.wlq_gemm_workspace_bytes(M, L.N, L.K, 4, 0, torch.cuda.current_device())
-        ws = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=DEV)
+        ws = torch.zeros(max(nbytes, 4), dtype=torch.uint8, device=DEV)  # zero-filled once, as documented
         stream = torch.cuda.current_stream().cuda_stream
-        if M == 1:
-            st = lib.wlq_gemv(t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), x.data_ptr(), out.data_ptr(),
-                              t["chunk_offsets"].data_ptr(), t["chunk_cols"].data_ptr(), t["chunk_vals"].data_ptr(),
-                              t["lora_B"].data_ptr(), H.data_ptr(), t["dora_gamma"].data_ptr(), None, 1.0, 8, L.N,
-                              L.K, 4, 128, ws.data_ptr(), ws.numel(), stream)
-        else:
-            st = lib.wlq_gemm(x.data_ptr(), t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), out.data_ptr(), M, L.N,
-                              L.K, 4, L.wpr, 128, t["chunk_offsets"].data_ptr(), t["chunk_cols"].data_ptr(),
-                              t["chunk_vals"].data_ptr(), H.data_ptr(), t["lora_B"].data_ptr(),
-                              t["dora_gamma"].data_ptr(), None, 1.0, 8, ws.data_ptr(), ws.numel(), stream)
-        assert st == 0, lib.wlq_last_error()
-        torch.cuda.synchronize()
-        assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+        for rep in range(2):  # the second call relies on the first leaving the arrival counters at zero
+            out.fill_(0)
+            if M == 1:
+                st = lib.wlq_gemv(t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), x.data_ptr(), out.data_ptr(),
+                                  t["chunk_offsets"].data_ptr(), t["chunk_cols"].data_ptr(),
+                                  t["chunk_vals"].data_ptr(), t["lora_B"].data_ptr(), H.data_ptr(),
+                                  t["dora_gamma"].data_ptr(), None, 1.0, 8, L.N, L.K, 4, 128, ws.data_ptr(),
+                                  ws.numel(), stream)
+            else:
+                st = lib.wlq_gemm(x.data_ptr(), t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), out.data_ptr(), M,
+                                  L.N, L.K, 4, L.wpr, 128, t["chunk_offsets"].data_ptr(), t["chunk_cols"].data_ptr(),
+                                  t["chunk_vals"].data_ptr(), H.data_ptr(), t["lora_B"].data_ptr(),
+                                  t["dora_gamma"].data_ptr(), None, 1.0, 8, ws.data_ptr(), ws.numel(), stream)
+            assert st == 0, lib.wlq_last_error()
+            torch.cuda.synchronize()
+            assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16)), f"M={M} call {rep}"
+            if nbytes:
+                assert int(ws[:16384].count_nonzero()) == 0, "arrival counters not reset"
+        # fused H (lora_A) through the C ABI, twice on the same workspace
+        if M <= 32:
+            nb = lib.wlq_gemm_workspace_bytes(M, L.N, L.K, 4, 8, torch.cuda.current_device())
+            wsf = torch.zeros(nb, dtype=torch.uint8, device=DEV)
+            yf, Hf = run_product(vw, L, x.cpu().numpy(), fused_h=True)
+            for rep in range(2):
+                out.fill_(0)
+                st = lib.wlq_gemm(x.data_ptr(), t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), out.data_ptr(), M,
+                                  L.N, L.K, 4, L.wpr, 128, t["chunk_offsets"].data_ptr(), t["chunk_cols"].data_ptr(),
+                                  t["chunk_vals"].data_ptr(), None, t["lora_B"].data_ptr(),
+                                  t["dora_gamma"].data_ptr(), t["lora_A"].data_ptr(), 1.0, 8, wsf.data_ptr(),
+                                  wsf.numel(), stream)
+                assert st == 0, lib.wlq_last_error()
+                torch.cuda.synchronize()
+                assert np.array_equal(out.cpu().numpy().view(np.uint16), yf.view(np.uint16)), f"fused M={M} {rep}"
+                assert int(wsf[:16384].count_nonzero()) == 0, "arrival counters not reset (fused)"
         # no workspace at all is valid (no split-K)
         out2 = torch.empty_like(out)
         st = lib.wlq_gemm(x.data_ptr(), t["q_packed"].data_ptr(), t["lut_c"].data_ptr(), out2.data_ptr(), M, L.N,
