@@ -6,18 +6,22 @@ projections (q, k, v, o, gate, up, down) at M = 1 activation row, 4-bit codes,
 fp16 LUTs per group of 128 columns, DoRA rank 16, 0.5% CSR outliers.  A step
 is one decoder layer's linear work as vLLM issues it: ``WLQLinearMethod.apply``
 on the four linear layers qkv_proj (q|k|v merged), o_proj, gate_up_proj
-(gate|up merged) and down_proj, captured in a HIP graph as vLLM's decode loop
-is; steps rotate over several copies of the weights (>= 512 MB in total) so
-HBM, not the 256 MB Infinity Cache, serves them.  ``value`` = code + LUT +
-outlier bytes per step / step time (GB/s); the bytes are those of the seven
+(gate|up merged) and down_proj.  As in vLLM's decode loop the steps are
+captured in one HIP graph: consecutive steps use different copies of the
+weights (like consecutive layers of the model; >= 512 MB in total, so HBM and
+not the 256 MB Infinity Cache serves them).  ``value`` = code + LUT + outlier
+bytes per step / step time (GB/s); the bytes are those of the seven
 projections.
 
-Also reported: the dominant kernel's roofline (the gate_proj decode product,
-timed with HIP events on its stream), the per-shape M = 1 rates, the M = 2048
-prefill GEMM rate in TFLOP/s against the dense fp16 MFMA peak (config 2), and
-the reference's CPU dequant+matmul path timed on this host (cpu_baseline).
+Also reported: the dominant kernel's roofline (the gate_up_proj decode
+product of the step, timed with HIP events on the stream it runs on; its HBM
+traffic comes from the rocprofv3 counter summary committed under profiles/),
+per-shape M = 1 rates, the M = 2048 prefill GEMM rate in TFLOP/s against the
+dense fp16 MFMA peak (config 2), and the reference's CPU dequant+matmul path
+timed on this host (cpu_baseline).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-cpu] [--no-gemm]
+       python bench.py --op NAME [--M 1] [--reps R]   (one product repeated, for rocprofv3)
 """
 from __future__ import annotations
 
@@ -48,32 +52,128 @@ def metric_name() -> str:
         return DEFAULT_METRIC
 
 
-def graph_of(fn):
+def graph_of(fns):
+    """One HIP graph running the callables in order (warmed up once outside capture)."""
     import torch
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        fn()
+        for fn in fns:
+            fn()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        fn()
+        for fn in fns:
+            fn()
     return g
 
 
-def time_graphs(graphs, iters):
+def time_graph(g, iters):
+    """ms per replay, HIP events on the stream the replays run on."""
     import torch
 
+    stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    e0.record()
-    for i in range(iters):
-        graphs[i % len(graphs)].replay()
-    e1.record()
+    e0.record(stream)
+    for _ in range(iters):
+        g.replay()
+    e1.record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / iters  # ms per replay
+    return e0.elapsed_time(e1) / iters
+
+
+PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "decode_gate_up_proj_m1_counters.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 counter
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the factor a plain copy kernel of
+    known size gives), or None when the summary is absent."""
+    try:
+        with open(PROFILE_SUMMARY) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        return None
+    return None
+
+
+def build_layers(dev, names=None):
+    from qwen_wlqfastshot_helen_beta_amd import synth
+
+    names = names or list(synth.QWEN25_7B_SHAPES)
+    layers = {n: synth.make_layer(*synth.QWEN25_7B_SHAPES[n], bits=4, group_size=128, rank=16, density=0.005,
+                                  seed=i) for i, n in enumerate(synth.QWEN25_7B_SHAPES) if n in names}
+    merged = {}
+    if all(n in layers for n in ("q_proj", "k_proj", "v_proj")):
+        merged["qkv_proj"] = synth.merge_layers([layers["q_proj"], layers["k_proj"], layers["v_proj"]])
+    if "o_proj" in layers:
+        merged["o_proj"] = layers["o_proj"]
+    if all(n in layers for n in ("gate_proj", "up_proj")):
+        merged["gate_up_proj"] = synth.merge_layers([layers["gate_proj"], layers["up_proj"]])
+    if "down_proj" in layers:
+        merged["down_proj"] = layers["down_proj"]
+    return layers, merged
+
+
+def op_fn(m, L, x, out):
+    """The decode/prefill product as vLLM's op issues it, with lora_A (H computed inside)."""
+    import torch
+
+    M = x.shape[0]
+
+    def fn():
+        if M == 1:
+            torch.ops.wlq_fastShot.gemv(m.q_packed_aligned, m.lut_c, x[0], out[0], L.N, L.K, 4, m.chunk_offsets,
+                                        m.chunk_cols, m.chunk_vals, m.lora_B, None, m.dora_gamma, 1.0, 128,
+                                        m.lora_A_f16)
+        else:
+            torch.ops.wlq_fastShot.gemm(x, m.q_packed_aligned, m.lut_c, out, L.N, L.K, 4, L.wpr, m.chunk_offsets,
+                                        m.chunk_cols, m.chunk_vals, None, m.lora_B, m.dora_gamma, 1.0, 128,
+                                        m.lora_A_f16)
+    return fn
+
+
+def run_single_op(args) -> int:
+    """--op: one product repeated eagerly over rotating weight copies (a profiling target)."""
+    import torch
+
+    import qwen_wlqfastshot_helen_beta_amd.vllm_wlq as vw
+    from qwen_wlqfastshot_helen_beta_amd import synth
+    from qwen_wlqfastshot_helen_beta_amd.vllm_wlq.linear_method import attach_synthetic
+
+    dev = torch.device("cuda:0")
+    if args.op == "copy":  # counter calibration: a plain device copy of known size
+        a = torch.empty(64 << 20, device=dev, dtype=torch.float32)  # 256 MiB
+        b = torch.empty_like(a)
+        for _ in range(args.reps):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(f"[bench] --op copy: {args.reps} copies of {a.numel() * 4} bytes done", flush=True)
+        return 0
+    base = {"qkv_proj": ["q_proj", "k_proj", "v_proj"], "gate_up_proj": ["gate_proj", "up_proj"]}
+    want = base.get(args.op, [args.op])
+    if not all(n in synth.QWEN25_7B_SHAPES for n in want):
+        print(f"bench.py: unknown --op {args.op}", file=sys.stderr)
+        return 2
+    layers, merged = build_layers(dev, want)
+    L = merged.get(args.op) or layers[args.op]
+    copies = max(2, math.ceil(512e6 / L.headline_bytes()) + 1)
+    mods = [attach_synthetic(torch.nn.Module(), L, dev) for _ in range(copies)]
+    vw.init_workspaces(L.N, L.K, dev)
+    x = torch.randn(args.M, L.K, device=dev).half()
+    out = torch.empty(args.M, L.N, device=dev, dtype=torch.float16)
+    fns = [op_fn(m, L, x, out) for m in mods]
+    for i in range(args.reps):
+        fns[i % copies]()
+    torch.cuda.synchronize()
+    print(f"[bench] --op {args.op} M={args.M}: {args.reps} launches done ({L.headline_bytes()} headline bytes each)",
+          flush=True)
+    return 0
 
 
 def main() -> int:
@@ -84,96 +184,86 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time M in {4, 8, 16, 32} per shape")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the M=2048 GEMM leg")
+    ap.add_argument("--op", default=None,
+                    help="only repeat this product (e.g. gate_up_proj) or 'copy' (256 MiB device copy), for profiling")
+    ap.add_argument("--M", type=int, default=1)
+    ap.add_argument("--reps", type=int, default=50)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU; multi-GPU runs are not part of it (use --gpus 1)",
               file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     import qwen_wlqfastshot_helen_beta_amd.vllm_wlq as vw
-    from qwen_wlqfastshot_helen_beta_amd import synth
     from qwen_wlqfastshot_helen_beta_amd.vllm_wlq.linear_method import WLQLinearMethod, attach_synthetic
+
+    if args.op:
+        return run_single_op(args)
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    names = list(synth.QWEN25_7B_SHAPES)
     t0 = time.time()
-    layers = {n: synth.make_layer(*synth.QWEN25_7B_SHAPES[n], bits=4, group_size=128, rank=16, density=0.005,
-                                  seed=i) for i, n in enumerate(names)}
+    layers, merged = build_layers(dev)
+    names = list(layers)
     log(f"[bench] synthetic layers built in {time.time() - t0:.1f}s")
-    merged = {"qkv_proj": synth.merge_layers([layers["q_proj"], layers["k_proj"], layers["v_proj"]]),
-              "o_proj": layers["o_proj"],
-              "gate_up_proj": synth.merge_layers([layers["gate_proj"], layers["up_proj"]]),
-              "down_proj": layers["down_proj"]}
     step_bytes = sum(L.headline_bytes() for L in layers.values())
     assert step_bytes == sum(L.headline_bytes() for L in merged.values())
     aux_bytes = sum(L.aux_bytes(1) for L in merged.values())
-    copies = max(2, math.ceil(512e6 / step_bytes) + 1)
+    copies = max(8, math.ceil(512e6 / step_bytes) + 1)
     method = WLQLinearMethod(vw.WLQFastShotConfig(bits=4, group_size=128))
     vnames = list(merged)
-    mods = [{n: attach_synthetic(torch.nn.Module(), layers[n], dev) for n in names} for _ in range(copies)]
     vmods = [{n: attach_synthetic(torch.nn.Module(), merged[n], dev) for n in vnames} for _ in range(copies)]
-    vw.init_workspaces(max(L.N for L in layers.values()), max(L.K for L in layers.values()), dev)
+    vw.init_workspaces(max(L.N for L in merged.values()), max(L.K for L in merged.values()), dev)
     xs = {K: torch.randn(1, K, device=dev).half() for K in {L.K for L in layers.values()}}
-    log(f"[bench] {copies} weight copies, {copies * step_bytes / 1e6:.0f} MB resident")
+    log(f"[bench] {copies} weight copies (layers), {copies * step_bytes / 1e6:.0f} MB resident")
 
-    # ---- headline: the decoder layer's four vLLM linear calls, one graph per weight copy
-    def layer_step(c):
-        def fn():
-            for n in vnames:
-                method.apply(vmods[c][n], xs[vmods[c][n].K])
-        return fn
+    # ---- headline: `copies` consecutive decoder layers' linear calls in one graph
+    def layer_fns(c):
+        return [(lambda n=n: method.apply(vmods[c][n], xs[vmods[c][n].K])) for n in vnames]
 
-    graphs = [graph_of(layer_step(c)) for c in range(copies)]
-    time_graphs(graphs, max(1, args.warmup))
-    torch.cuda.synchronize()
+    g_layers = graph_of([fn for c in range(copies) for fn in layer_fns(c)])
+    time_graph(g_layers, max(1, args.warmup // copies + 1))
+    replays = max(1, args.steps // copies)
     wall0 = time.perf_counter()
-    ms_step = time_graphs(graphs, args.steps)
+    ms_step = time_graph(g_layers, replays) / copies
     wall = time.perf_counter() - wall0
+    steps_timed = replays * copies
     value = step_bytes / (ms_step * 1e-3) / 1e9
     log(f"[bench] layer step {ms_step * 1e3:.2f} us -> {value:.0f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of HBM peak),"
-        f" wall {wall:.3f}s for {args.steps} steps")
+        f" wall {wall:.3f}s for {steps_timed} steps")
 
-    # ---- per-shape decode products (the op alone), M = 1 (and the config-1 sweep)
-    def op_graphs(n, M):
-        L = layers[n]
+    # ---- per-shape products: `copies` launches of one product in one graph
+    def op_time(L, M, reps=20):
+        mods = [attach_synthetic(torch.nn.Module(), L, dev) for _ in range(copies)]
         xm = torch.randn(M, L.K, device=dev).half()
-        outs = [torch.empty(M, L.N, device=dev, dtype=torch.float16) for _ in range(copies)]
-        def fn_for(c):
-            m = mods[c][n]
-
-            def fn():  # the op with lora_A: DoRA H computed inside the product
-                if M == 1:
-                    torch.ops.wlq_fastShot.gemv(m.q_packed_aligned, m.lut_c, xm[0], outs[c][0], L.N, L.K, 4,
-                                                m.chunk_offsets, m.chunk_cols, m.chunk_vals, m.lora_B, None,
-                                                m.dora_gamma, 1.0, 128, m.lora_A_f16)
-                else:
-                    torch.ops.wlq_fastShot.gemm(xm, m.q_packed_aligned, m.lut_c, outs[c], L.N, L.K, 4, L.wpr,
-                                                m.chunk_offsets, m.chunk_cols, m.chunk_vals, None, m.lora_B,
-                                                m.dora_gamma, 1.0, 128, m.lora_A_f16)
-            return fn
-
-        return [graph_of(fn_for(c)) for c in range(copies)]
+        out = torch.empty(M, L.N, device=dev, dtype=torch.float16)
+        g = graph_of([op_fn(m, L, xm, out) for m in mods])
+        time_graph(g, 2)
+        ms = time_graph(g, reps) / copies
+        del g, mods
+        return ms
 
     per_shape = {}
     Ms = [1, 4, 8, 16, 32] if args.sweep else [1]
-    for n in names:
+    shapes = dict(layers)
+    shapes["gate_up_proj"] = merged["gate_up_proj"]
+    for n, L in shapes.items():
         for M in Ms:
-            gs = op_graphs(n, M)
-            time_graphs(gs, 20)
-            ms = time_graphs(gs, 200)
-            gbs = layers[n].headline_bytes() / (ms * 1e-3) / 1e9
+            if n == "gate_up_proj" and M != 1:
+                continue
+            ms = op_time(L, M)
+            gbs = L.headline_bytes() / (ms * 1e-3) / 1e9
             per_shape[f"{n}_M{M}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                       "frac": round(gbs / HBM_PEAK_GBS, 4)}
-            log(f"[bench] {n:9s} M={M:2d}: {ms * 1e3:8.2f} us  {gbs:7.0f} GB/s")
-    dom = per_shape["gate_proj_M1"]
+            log(f"[bench] {n:12s} M={M:2d}: {ms * 1e3:8.2f} us  {gbs:7.0f} GB/s")
+    dom = per_shape["gate_up_proj_M1"]
     roofline = {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "wlq skinny decode product, gate_proj 18944x3584 M=1 (+ split-K reduce)",
-                "bytes_per_launch": layers["gate_proj"].headline_bytes(), "avg_us": dom["us"]}
+                "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "kernel": "skinny4_kernel (decode product incl. DoRA x.A^T blocks and in-kernel epilogue), "
+                          "gate_up_proj 37888x3584 M=1",
+                "bytes_per_launch": merged["gate_up_proj"].headline_bytes(), "avg_us": dom["us"]}
 
     # ---- prefill GEMM, M = 2048 (config 2)
     gemm = None
@@ -182,9 +272,7 @@ def main() -> int:
         tot_flop, tot_ms, rows = 0.0, 0.0, {}
         for n in names:
             L = layers[n]
-            gs = op_graphs(n, M)
-            time_graphs(gs, 3)
-            ms = time_graphs(gs, 10)
+            ms = op_time(L, M, reps=3)
             fl = 2.0 * M * L.N * L.K
             tot_flop += fl
             tot_ms += ms
@@ -203,11 +291,11 @@ def main() -> int:
         torch.set_num_threads(threads)
         cl = [cpu_path.CpuLayer(layers[n]) for n in names]
         xk = {K: x.cpu() for K, x in xs.items()}
-        t_full, t_cached = cpu_path.time_layers(cl, xk, reps=2)
+        t_full, t_cached = cpu_path.time_layers(cl, xk, reps=5)
         cpu = {"value": round(step_bytes / t_full / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
                "kind": "port",
-               "sample": "one pass over the 7 projections at M=1 (dequant+matmul per call, median of 2); "
-                         f"{t_full:.2f} s/pass, matmul-only with cached W0 {t_cached:.3f} s/pass",
+               "sample": "the 7 projections at M=1, dequant+matmul per call as the reference's CPU path does "
+                         f"(median of 5 passes, {t_full:.2f} s/pass); matmul-only with cached W0 {t_cached:.3f} s/pass",
                "matmul_only_GB/s": round(step_bytes / t_cached / 1e9, 3)}
         log(f"[bench] cpu baseline: {t_full:.2f} s/pass ({cpu['value']} GB/s) on {cpu['cores']} threads")
 
@@ -216,7 +304,7 @@ def main() -> int:
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps_timed,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
@@ -226,9 +314,9 @@ def main() -> int:
         "data": "synthetic (seeded metalog LUTs, uniform 4-bit codes, random DoRA/outliers)",
         "config": {"workload": "cfg1: Qwen2.5-7B decoder layer at M=1 (q,k,v,o,gate,up,down issued as vLLM's "
                                "qkv/o/gate_up/down linears); 4-bit, LUT group 128, DoRA r=16, 0.5% CSR outliers; "
-                               "HIP-graph step over weight copies",
+                               "consecutive layers on distinct weight copies in one HIP graph",
                    "M": 1, "bits": 4, "group_size": 128, "rank": 16, "outlier_density": 0.005,
-                   "bytes_per_step": step_bytes, "aux_bytes_per_step": aux_bytes, "weight_copies": copies},
+                   "bytes_per_step": step_bytes, "aux_bytes_per_step": aux_bytes, "layers_per_graph": copies},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,
