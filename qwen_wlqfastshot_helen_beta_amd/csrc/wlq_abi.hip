@@ -198,6 +198,8 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
   L.wpr = (int)wlq_words_per_row(K, bits);
   L.chunk = wlq_chunk_width(bits);
   L.nch = (int)((K + L.chunk - 1) / L.chunk);
+  // sized as if outliers are present (the GEMM's prepared outlier entries); never dereferenced
+  L.offsets = reinterpret_cast<const int32_t*>(&L);
   const int cus = device >= 0 ? cu_count_for(device) : current_cu_count();
   const size_t unlimited = ~(size_t)0;
   const bool skinny = M <= wlq::skinny_max_m();

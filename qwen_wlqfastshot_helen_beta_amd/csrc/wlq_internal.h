@@ -35,7 +35,8 @@ struct SplitPlan {
   int splits;               // blocks along K
   int slabs_per_split;      // K range per block, in slabs
   int seg_slabs;            // activation staging segment, in slabs
-  size_t workspace_bytes;   // fp32 partials needed (0 when splits == 1)
+  size_t workspace_bytes;   // fp32 partials (0 when splits == 1) + aux_bytes
+  size_t aux_bytes;         // GEMM: prepared outlier entries after the partials (0: not used)
 };
 
 // The first kSyncBytes of a caller's workspace hold arrival counters of the decode
