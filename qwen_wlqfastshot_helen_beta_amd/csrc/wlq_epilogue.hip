@@ -1,8 +1,8 @@
 // Output epilogues.
 //
-// * splitk_reduce_kernel: y[i, n] = fp16_rn((sum_s partial[s, i, n] + scale * H[i,:].B[n,:]) * gamma[n]),
-//   the partials summed in split order (deterministic).  Reference behaviour:
-//   reduce_split_k_dora_kernel (csrc/gemv_kernel.cu:322-353), generalized to M rows.
+// * splitk_sum_kernel: y = fp16_rn(sum_s partial[s]) for the prefill GEMM's split-K partials, which
+//   already carry the DoRA term and gamma; summed in split order (deterministic).  Reference
+//   behaviour: reduce_split_k_dora_kernel (csrc/gemv_kernel.cu:322-353), generalized to M rows.
 // * dora_epilogue_kernel: the in-place pass of the reference's M >= 16 path,
 //   out = fp16_rn((fp16 out + scale * H.B) * gamma) (csrc/gemm_kernel.cu:447-473).
 #include "wlq_device.h"
@@ -19,17 +19,35 @@ __device__ __forceinline__ float dora_dot(const Dora& D, int i, int n) {
   return ls;
 }
 
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ partial, int splits, int M,
-                                                            int N, const Dora D, uint16_t* __restrict__ out) {
-  const size_t total = (size_t)M * N;
-  const size_t plane = total;
-  for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
-    const int i = (int)(idx / (size_t)N);
-    const int n = (int)(idx - (size_t)i * N);
-    float v = 0.f;
-    for (int s = 0; s < splits; ++s) v += partial[(size_t)s * plane + idx];
-    if (D.r > 0) v = (v + D.scale * dora_dot(D, i, n)) * h2f(D.gamma[n]);
-    out[idx] = f2h_rn(v);
+// y = fp16_rn(sum_s partial[s]) over M*N values, partials summed in split order.
+// VEC: four consecutive values per thread (16-byte partial loads, one 8-byte store).
+template <bool VEC>
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ partial, int splits,
+                                                         size_t total, uint16_t* __restrict__ out) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  if (VEC) {
+    const size_t quads = total / 4;
+    const float4* p4 = reinterpret_cast<const float4*>(partial);
+    for (size_t q = (size_t)blockIdx.x * 256 + threadIdx.x; q < quads; q += stride) {
+      float4 v = p4[q];
+      for (int s = 1; s < splits; ++s) {
+        const float4 w = p4[(size_t)s * quads + q];
+        v.x += w.x;
+        v.y += w.y;
+        v.z += w.z;
+        v.w += w.w;
+      }
+      uint2 o;
+      o.x = (uint32_t)f2h_rn(v.x) | ((uint32_t)f2h_rn(v.y) << 16);
+      o.y = (uint32_t)f2h_rn(v.z) | ((uint32_t)f2h_rn(v.w) << 16);
+      reinterpret_cast<uint2*>(out)[q] = o;
+    }
+  } else {
+    for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += stride) {
+      float v = partial[idx];
+      for (int s = 1; s < splits; ++s) v += partial[(size_t)s * total + idx];
+      out[idx] = f2h_rn(v);
+    }
   }
 }
 
@@ -155,11 +173,17 @@ unsigned grid_for(size_t total) {
 
 }  // namespace
 
-hipError_t launch_splitk_reduce(const float* partial, int splits, int M, int N, const Dora& D, uint16_t* out,
-                                hipStream_t stream) {
+hipError_t launch_splitk_sum(const float* partial, int splits, int M, int N, uint16_t* out, hipStream_t stream) {
   if (M <= 0 || N <= 0) return hipSuccess;
-  const dim3 grid(grid_for((size_t)M * N));
-  hipLaunchKernelGGL(splitk_reduce_kernel, grid, dim3(256), 0, stream, partial, splits, M, N, D, out);
+  const size_t total = (size_t)M * N;
+  const bool vec = (total % 4 == 0) && ((reinterpret_cast<uintptr_t>(partial) & 15) == 0) &&
+                   ((reinterpret_cast<uintptr_t>(out) & 7) == 0);
+  if (vec)
+    hipLaunchKernelGGL(splitk_sum_kernel<true>, dim3(grid_for(total / 4)), dim3(256), 0, stream, partial, splits,
+                       total, out);
+  else
+    hipLaunchKernelGGL(splitk_sum_kernel<false>, dim3(grid_for(total)), dim3(256), 0, stream, partial, splits,
+                       total, out);
   return hipGetLastError();
 }
 

@@ -5,25 +5,37 @@
 // HGEMM, separate DoRA pass) and gemm_metalog_dora_kernel's overwrite semantics
 // (csrc/gemm_kernel.cu:204-228).  W is never materialized in HBM.
 //
-// Block tile 256 (M) x 128 (N), K step 64, 512 threads = 8 waves in a 4x2
-// arrangement, each wave a 64x64 sub-tile of V_MFMA_F32_16X16X32_F16.  The W
-// tile is dequantized once per block and shared by the 256 activation rows.
+// Block tile 256 (M) x 128 (N), K step 64, 512 threads in two roles:
 //
-// Pipeline per K step: the global loads of step k+2 (activations, code
-// windows, group LUTs) are issued into registers, the MFMAs of step k read LDS
-// buffer k%2, then step k+1's registers are written to the other LDS buffer:
-// activations permuted to column order P, codes expanded through their LUT byte
-// planes (4 threads per W row, 16 columns each), outliers overwritten (the
-// reference's W0 = e5m2 << 8 at outlier positions).  One barrier per step.
-// Outlier entries of the block's 128 rows are staged per 512-column chunk
-// (640 for 3-bit) into LDS, one chunk ahead, in phases spread over the chunk's
-// first steps (offsets, counts, prefix, entries), so no dependent global load
-// sits in the loop.
+// * 4 consumer waves (one per SIMD), each a 128x64 sub-tile of
+//   V_MFMA_F32_16X16X32_F16 (accumulators in AGPRs): per K step they read the
+//   step's fragments from LDS and issue 64 MFMAs each, nothing else.
+// * 4 producer waves (one per SIMD) fill the other LDS buffer with the next
+//   step meanwhile: activations permuted to column order P, codes expanded
+//   through their LUT byte planes (two threads per W row, 32 columns each),
+//   outliers overwritten (the reference's W0 = e5m2 << 8 at outlier positions).
+//   Their global loads run four steps ahead in registers (two for 3-bit).
 //
-// DoRA: with one split, the low-rank term s * H . B^T is added in the
-// epilogue with V_MFMA_F32_16X16X4_F32 (fp32 operands, exact products) and
-// the block writes fp16((acc + s H B^T) * gamma); with split-K the partials go
-// to an fp32 workspace and splitk_reduce_kernel applies the epilogue.
+// So each SIMD runs one MFMA wave and one VALU wave side by side; one barrier
+// per step hands the buffers over.  The roles run separate loops (the same
+// number of barriers), so neither carries the other's registers.
+//
+// LDS tiles are unpadded 128-byte rows whose 16-byte units are XOR-swizzled by
+// row: unit u of row r sits at u ^ swz(r), swz(r) = ((r >> 1) & 7) ^ ((r >> 3) & 1).
+// The 16 rows of an MFMA fragment read land on distinct bank groups, and so do the
+// producers' stores, whose activation loads stay 128-byte coalesced rows.  The
+// consumers issue all fragment reads of a step before its MFMAs need them.
+//
+// The producer loop runs one 512-column outlier chunk (640 for 3-bit) per trip
+// with its steps unrolled, so everything tied to chunk boundaries is fixed at
+// compile time.  Outlier entries of the block's 128 rows are prepared per
+// (N tile, chunk) by tile_entries_kernel (row prefix + entries in row order),
+// staged into LDS one chunk ahead, and each W thread walks its row's entries.
+//
+// DoRA: the low-rank term s * H . B^T is added in the epilogue of split 0 with
+// V_MFMA_F32_16X16X4_F32 (fp32 operands, exact products) and every split scales
+// by gamma; one split writes fp16((acc + s H B^T) * gamma), several write fp32
+// partials that splitk_sum_kernel adds and rounds.
 //
 // Blocks are mapped so that each XCD works through a contiguous range of
 // tiles, N-tile major: consecutive blocks of one XCD share W tiles in its L2.
@@ -40,7 +52,7 @@ constexpr int BM = 256;
 constexpr int BN = 128;
 constexpr int BK = 64;
 constexpr int NT = 512;
-constexpr int LDS_ROW = BK + 8;  // halves per LDS row (16-byte pad)
+constexpr int NP = 256;          // producer threads (waves 4..7)
 constexpr int kEntCap = 2048;    // outlier entries of one (N tile, chunk) held in LDS
 constexpr int kPosWords = 132;   // row prefix (BN + 1 used), padded to 16 bytes
 constexpr int kSlotWords = kPosWords + kEntCap;  // one (N tile, chunk) slot of the prepared entries
@@ -70,52 +82,99 @@ struct GemmArgs {
 };
 
 struct GemmSmem {
-  uint16_t a[2][BM * LDS_ROW];
-  uint16_t b[2][BN * LDS_ROW];
+  uint16_t a[2][BM * BK];
+  uint16_t b[2][BN * BK];
   uint32_t ent[2][kEntCap];   // col | val << 16, the tile's rows in order
   int pos[2][kPosWords];      // row start inside ent (exclusive prefix), pos[BN] = total
 };
 
 __device__ __forceinline__ int group_of(int col, uint32_t magic) { return (int)__umulhi((uint32_t)col, magic); }
 
-// 16-column code piece starting at column c16 (c16 % 16 == 0) of a packed row:
-// the words that hold it (clamped inside the row; columns past K meet zero
-// activations) and its two 8-column blocks expanded to fp16 pairs in order P.
+// Swizzle of a tile row (depends on row % 16 only).
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) & 7) ^ ((row >> 3) & 1); }
+
+// Buffer resources (raw, stride 0): a load whose offset is at or past the
+// resource's size returns zeros, which is how activation columns past K and
+// code words past the last row read as harmless values without per-lane checks.
+constexpr int kRsrcWord3 = 0x00020000;         // raw buffer, 32-bit data format (gfx9)
+constexpr uint32_t kOutOfRange = 0x80000000u;  // past every resource (sizes are < 2^31 bytes)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+// LUT modes: one LUT per row (loaded once); groups of G % 128 == 0 columns (a group
+// spans two K steps: planes built on even steps); G % 64 == 0 (one group per step);
+// G % 32 == 0 (one group per thread's 32 columns of a step).
+enum LutMode : int { kLutRow = 0, kLutPair = 1, kLutStep = 2, kLutHalf = 3 };
+
+// Code words of one thread's 32 columns of a step.
+template <int BITS> struct StepCodes { static constexpr int kWords = BITS == 4 ? 4 : BITS == 3 ? 6 : BITS == 2 ? 2 : 1; };
+
+// Columns c0 .. c0 + 31 (c0 % 32 == 0) of the row at byte offset qbase.
 template <int BITS>
-__device__ __forceinline__ void load_piece16(const uint32_t* __restrict__ qrow, int c16, int wpr, uint32_t w[3]) {
-  if constexpr (BITS == 4) {
-    const u32x2_t v = *reinterpret_cast<const u32x2_t*>(qrow + min(c16 >> 3, wpr - 2));
-    w[0] = v.x; w[1] = v.y; w[2] = 0u;
-  } else if constexpr (BITS == 2) {
-    w[0] = qrow[min(c16 >> 4, wpr - 1)]; w[1] = 0u; w[2] = 0u;
-  } else if constexpr (BITS == 1) {
-    w[0] = qrow[min(c16 >> 5, wpr - 1)]; w[1] = 0u; w[2] = 0u;
-  } else {
-    const int wi = c16 / 10;
+__device__ __forceinline__ void load_codes(__amdgpu_buffer_rsrc_t rq, uint32_t qbase, int c0,
+                                           uint32_t w[StepCodes<BITS>::kWords]) {
+  if constexpr (BITS == 4) {  // words c0/8 .. + 3
+    const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(rq, (int)(qbase + (uint32_t)(c0 >> 1)), 0, 0);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  } else if constexpr (BITS == 2) {  // words c0/16, + 1
+    const u32x2_t a = __builtin_amdgcn_raw_buffer_load_b64(rq, (int)(qbase + (uint32_t)(c0 >> 2)), 0, 0);
+    w[0] = a.x; w[1] = a.y;
+  } else if constexpr (BITS == 1) {  // word c0/32
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rq, (int)(qbase + (uint32_t)(c0 >> 3)), 0, 0);
+  } else {  // 3-bit: per 16-column piece p the three words from (c0 + 16 p) / 10
 #pragma unroll
-    for (int j = 0; j < 3; ++j) w[j] = qrow[min(wi + j, wpr - 1)];
+    for (int p = 0; p < 2; ++p) {
+      const uint32_t off = qbase + 4u * (uint32_t)((c0 + 16 * p) / 10);
+#pragma unroll
+      for (int j = 0; j < 3; ++j) w[3 * p + j] = __builtin_amdgcn_raw_buffer_load_b32(rq, (int)(off + 4u * j), 0, 0);
+    }
   }
 }
 
-template <int BITS, int BLK>
-__device__ __forceinline__ void dequant_piece16(const uint32_t w[3], int c16, const LutPlanes<BITS>& t,
-                                                uint32_t out[4]) {
+template <int BITS>
+__device__ __forceinline__ void lut_load_buf(LutRaw<BITS>& raw, __amdgpu_buffer_rsrc_t rl, uint32_t voff,
+                                             uint32_t soff) {
   if constexpr (BITS == 4) {
-    dequant_word4(w[BLK], t, out);
+    const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(rl, (int)voff, (int)soff, 0);
+    const u32x4_t b = __builtin_amdgcn_raw_buffer_load_b128(rl, (int)(voff + 16u), (int)soff, 0);
+    raw.r[0] = a.x; raw.r[1] = a.y; raw.r[2] = a.z; raw.r[3] = a.w;
+    raw.r[4] = b.x; raw.r[5] = b.y; raw.r[6] = b.z; raw.r[7] = b.w;
+  } else if constexpr (BITS == 3) {
+    const u32x4_t a = __builtin_amdgcn_raw_buffer_load_b128(rl, (int)voff, (int)soff, 0);
+    raw.r[0] = a.x; raw.r[1] = a.y; raw.r[2] = a.z; raw.r[3] = a.w;
+  } else if constexpr (BITS == 2) {
+    const u32x2_t a = __builtin_amdgcn_raw_buffer_load_b64(rl, (int)voff, (int)soff, 0);
+    raw.r[0] = a.x; raw.r[1] = a.y;
   } else {
+    raw.r[0] = __builtin_amdgcn_raw_buffer_load_b32(rl, (int)voff, (int)soff, 0);
+  }
+}
+
+// 8 columns (unit U of the thread's 32, columns c0 + 8U ..) expanded to fp16 pairs in order P.
+template <int BITS, int U>
+__device__ __forceinline__ void dequant_unit(const uint32_t* w, int c0, const LutPlanes<BITS>& t, uint32_t out[4]) {
+  if constexpr (BITS == 4) {
+    dequant_word4(w[U], t, out);
+  } else {
+    constexpr int P = U >> 1;    // 16-column piece
+    constexpr int BLK = U & 1;   // 8-column block inside the piece
     uint32_t code[8];
     if constexpr (BITS == 2) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) code[j] = (w[0] >> (2 * (8 * BLK + j))) & 3u;
+      for (int j = 0; j < 8; ++j) code[j] = (w[P] >> (2 * (8 * BLK + j))) & 3u;
     } else if constexpr (BITS == 1) {
-      const uint32_t v = w[0] >> ((c16 & 31) + 8 * BLK);
+      const uint32_t v = w[0] >> (16 * P + 8 * BLK);
 #pragma unroll
       for (int j = 0; j < 8; ++j) code[j] = (v >> j) & 1u;
     } else {  // 3-bit: slot s0 = c16 % 10 of word c16 / 10; codes up to slot s0 + 15 < 25
+      const int c16 = c0 + 16 * P;
       const int s0 = c16 - (c16 / 10) * 10;
+      const uint32_t* pw = w + 3 * P;
       // the 25 slots of three words as two 64-bit windows (values only: no indexed access)
-      const uint64_t lo = (uint64_t)w[0] | ((uint64_t)w[1] << 30);   // slots 0..19 at 3 bits each
-      const uint64_t hi = (uint64_t)w[1] | ((uint64_t)w[2] << 30);   // slots 10..29
+      const uint64_t lo = (uint64_t)pw[0] | ((uint64_t)pw[1] << 30);   // slots 0..19 at 3 bits each
+      const uint64_t hi = (uint64_t)pw[1] | ((uint64_t)pw[2] << 30);   // slots 10..29
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int idx = s0 + 8 * BLK + j;
@@ -130,29 +189,34 @@ __device__ __forceinline__ void dequant_piece16(const uint32_t w[3], int c16, co
   }
 }
 
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
 // ------------------------------------------------------------------ kernel
 
-// Registers carrying one K step from global memory to LDS.
+// Producer registers carrying one K step from global memory to LDS.
 template <int BITS>
 struct StepRegs {
-  u32x4_t x[4];      // activation 16-byte units u = tid + NT * j
-  uint32_t cw[3];    // words holding this thread's 16 code columns
-  LutRaw<BITS> lr;   // LUT entries of the piece's group (group LUTs)
+  u32x4_t x[8];                             // activation units u = ptid + NP * j
+  uint32_t cw[StepCodes<BITS>::kWords];     // code words of the thread's 32 columns
+  LutRaw<BITS> lr;                          // group LUT of the step
 };
 
-template <int BITS, bool PER_ROW, bool HAS_CSR, bool X_VEC>
+template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC>
 __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   constexpr int NCB = 1 << BITS;
+  constexpr int SPC = (BITS == 3 ? 640 : 512) / BK;  // K steps per outlier chunk (even)
+  static_assert(SPC % 2 == 0, "register sets keep their step parity");
   extern __shared__ __align__(16) unsigned char smem_raw[];
   GemmSmem& sm = *reinterpret_cast<GemmSmem*>(smem_raw);
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1;  // 0..3: 64-row slice of the M tile
-  const int wn = wave & 1;   // 0..1: 64-column slice of the N tile
-  const int r = lane & 15;
-  const int kq = lane >> 4;
 
   // tile of this block: XCD-contiguous ranges, N-tile major
   const int split = blockIdx.x / a.tiles;
@@ -165,39 +229,190 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   const int m0 = (t - tn * a.tiles_m) * BM;
   const int n0 = tn * BN;
 
+  // K range: whole outlier chunks; steps past K (the last chunk's tail) read zero
+  // activations and add nothing
   const int ksteps_total = (a.K + BK - 1) / BK;
-  const int kt_begin = split * a.ksteps_per_split;  // whole chunks (the planner aligns splits)
+  const int kt_begin = split * a.ksteps_per_split;
   const int kt_end = min(ksteps_total, kt_begin + a.ksteps_per_split);
-  const int kt_last = max(kt_end - 1, kt_begin);
+  const int ck_begin = kt_begin / SPC;
+  const int ck_end = (kt_end + SPC - 1) / SPC;
+  const bool has_work = kt_begin < kt_end;
 
-  // W producer role: row nl of the tile, 16 columns [16 qq, 16 qq + 16) of each step
-  const int nl = tid >> 2;
-  const int qq = tid & 3;
+  // Prepared outlier lists are used when every chunk of this block's range fits its
+  // slot; otherwise the producers read the CSR arrays directly (a separate loop, so
+  // the hot loop carries no data-dependent loads).
+  __shared__ int s_direct;
+  bool prepared = false;
+  if constexpr (HAS_CSR) {
+    if (a.tent != nullptr) {
+      if (tid == 0) s_direct = 0;
+      __syncthreads();
+      if (tid < ck_end - ck_begin &&
+          (int)a.tent[((size_t)tn * a.nch + ck_begin + tid) * kSlotWords + BN] > kEntCap)
+        s_direct = 1;
+      __syncthreads();
+      prepared = s_direct == 0;
+    }
+  }
+  // barriers of the prologue: staging, plus the entries of the first chunk when prepared
+  const int prologue_barriers = (HAS_CSR && prepared) ? 2 : 1;
+
+  if (wave < 4) {
+    // ------------------------------------------------------------ consumer waves
+    const int lane = tid & 63;
+    const int wm = wave >> 1;  // 0..1: 128-row slice of the M tile
+    const int wn = wave & 1;   // 0..1: 64-column slice of the N tile
+    const int r = lane & 15;
+    const int kq = lane >> 4;
+
+    float4_t acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    if (has_work) {
+      // fragment rows 16 i + r of the wave's slices; k unit 4 ks + kq, swizzled by row
+      const int a_frag = (128 * wm + r) * BK;
+      const int b_frag = (64 * wn + r) * BK;
+      const int f_unit0 = 8 * ((0 + kq) ^ swz(r));
+      const int f_unit1 = 8 * ((4 + kq) ^ swz(r));
+      for (int i = 0; i < prologue_barriers; ++i) __syncthreads();
+      const int steps = (ck_end - ck_begin) * SPC;
+      for (int st = 0; st < steps; ++st) {
+        const int buf = st & 1;
+        // all fragments of the step in flight early: ks = 0 first, ks = 1 spread over
+        // the ks = 0 MFMAs, so no MFMA waits for an LDS round trip of its own
+        u32x4_t af[2][8], bf[2][4];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int fu = ks ? f_unit1 : f_unit0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            bf[ks][j] = *reinterpret_cast<const u32x4_t*>(&sm.b[buf][b_frag + 16 * j * BK + fu]);
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            af[ks][i] = *reinterpret_cast<const u32x4_t*>(&sm.a[buf][a_frag + 16 * i * BK + fu]);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(af[ks][i], bf[ks][j], acc[i][j]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);  // DS read: ks = 0 fragments
+#pragma unroll
+        for (int q = 0; q < 12; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read: a ks = 1 fragment
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 40, 0);
+        __syncthreads();
+      }
+    }
+
+    // Epilogue.  Lane holds D[4*kq + e][r] of every 16x16 tile (i, j).  Split 0 adds the
+    // DoRA term and every split scales by gamma (the split-K sum of gamma-scaled partials
+    // is gamma times the sum), so the split-K reduce is a plain sum.
+    if (a.r > 0 && split == 0) {
+      // acc += s * H . B^T on the matrix core in fp32 (V_MFMA_F32_16X16X4_F32: A = s*H,
+      // lane l holds row l%16, k = l/16; B = B^T, lane l holds k = l/16, column l%16).
+      for (int kr = 0; kr < a.r; kr += 4) {
+        const int k = kr + kq;
+        const int kc = min(k, a.r - 1);
+        float hv[8], bv[4];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int ma = m0 + 128 * wm + 16 * i + r;
+          const float h = a.H[(size_t)min(ma, a.M - 1) * a.r + kc];
+          hv[i] = (ma < a.M && k < a.r) ? a.scale * h : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int n = n0 + 64 * wn + 16 * j + r;
+          const float b = h2f(a.B[(size_t)min(n, a.N - 1) * a.r + kc]);
+          bv[j] = (n < a.N && k < a.r) ? b : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[i], bv[j], acc[i][j], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + 64 * wn + 16 * j + r;
+      if (n >= a.N) continue;
+      const float g = a.r > 0 ? h2f(a.gamma[n]) : 1.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int m = m0 + 128 * wm + 16 * i + 4 * kq + e;
+          if (m >= a.M) continue;
+          const float v = a.r > 0 ? acc[i][j][e] * g : acc[i][j][e];
+          if (a.splits == 1)
+            a.out[(size_t)m * a.N + n] = f2h_rn(v);
+          else
+            a.partial[((size_t)split * a.M + m) * a.N + n] = v;
+        }
+      }
+    }
+    return;
+  }
+
+  // -------------------------------------------------------------- producer waves
+  if (!has_work) return;
+  const int ptid = tid - 4 * 64;
+
+  // A producer: units u = ptid + NP * j, row u / 8 = ptid / 8 + 32 j, columns 8 (ptid % 8) + [0, 8)
+  // (eight lanes read one 128-byte row)
+  const int xc8 = ptid & 7;
+  const int xrow0 = ptid >> 3;
+  const int xoff = xrow0 * BK + 8 * (xc8 ^ swz(xrow0));  // rows + 32 j share the swizzle
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.X, (uint32_t)((size_t)a.M * a.K * 2));
+  uint32_t xbase[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    xbase[j] = (uint32_t)(((size_t)min(m0 + xrow0 + 32 * j, a.M - 1) * a.K + 8 * xc8) * 2);
+  const int xlim = a.K - 8 * xc8;  // the unit holds activations while k0 < xlim
+
+  // W producer: row nl of the tile, columns [32 h, 32 h + 32) of each step
+  const int nl = ptid >> 1;
+  const int hh = ptid & 1;
   const int nb = n0 + nl;
   const bool brow_ok = nb < a.N;
   const int nbc = brow_ok ? nb : (a.N - 1);
-  const uint32_t* qrow = a.q + (size_t)nbc * a.wpr;
-  const uint16_t* lrow = a.lut + (size_t)nbc * a.ng * NCB;
+  const int wsw = swz(nl);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q, (uint32_t)((size_t)a.N * a.wpr * 4));
+  const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.lut, (uint32_t)((size_t)a.N * a.ng * NCB * 2));
+  const uint32_t qbase = (uint32_t)nbc * (uint32_t)a.wpr * 4u;
+  const uint32_t lbase = (uint32_t)nbc * (uint32_t)(a.ng * NCB * 2);
 
   LutPlanes<BITS> pl_row;
-  if constexpr (PER_ROW) {
+  if constexpr (LUTM == kLutRow) {
     LutRaw<BITS> raw;
-    lut_load<BITS>(raw, lrow);
+    lut_load_buf<BITS>(raw, rl, lbase, 0u);
     pl_row = lut_planes<BITS>(raw);
   }
+  LutPlanes<BITS> pl_pair;  // kLutPair: planes of the current two-step group
 
-  auto load_step = [&](StepRegs<BITS>& S, int kt) __attribute__((always_inline)) {
+  // Loads of step kt into S.  EVEN: the step's index from the range start is even.
+  auto load_step = [&](StepRegs<BITS>& S, int kt, auto even_c) __attribute__((always_inline)) {
+    constexpr bool kEven = decltype(even_c)::value;
     const int k0 = kt * BK;
+    if constexpr (X_VEC) {
+      const bool in = k0 < xlim;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int u = tid + NT * j;
-      const int row = u >> 3;
-      const int col = k0 + 8 * (u & 7);
-      if constexpr (X_VEC) {  // clamped, unconditional; out-of-range units are zeroed when stored
-        const int m = min(m0 + row, a.M - 1);
-        S.x[j] = *reinterpret_cast<const u32x4_t*>(a.X + (size_t)m * a.K + min(col, a.K - 8));
-      } else {
-        const int m = m0 + row;
+      for (int j = 0; j < 8; ++j)
+        S.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(in ? xbase[j] + 2u * (uint32_t)k0 : kOutOfRange),
+                                                       0, 0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int m = m0 + xrow0 + 32 * j;
+        const int col = k0 + 8 * xc8;
         u32x4_t v = {0u, 0u, 0u, 0u};
         if (m < a.M) {
           const uint16_t* src = a.X + (size_t)m * a.K + col;
@@ -212,66 +427,84 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
         S.x[j] = v;
       }
     }
-    const int c16 = k0 + 16 * qq;
-    load_piece16<BITS>(qrow, c16, a.wpr, S.cw);
-    if constexpr (!PER_ROW) {
-      const int g = min(group_of(c16, a.g_magic), a.ng - 1);
-      lut_load<BITS>(S.lr, lrow + g * NCB);
+    const int c0 = k0 + 32 * hh;
+    load_codes<BITS>(rq, qbase, c0, S.cw);
+    if constexpr (LUTM == kLutStep || (LUTM == kLutPair && kEven)) {
+      const int g = min(group_of(k0, a.g_magic), a.ng - 1);  // uniform
+      lut_load_buf<BITS>(S.lr, rl, lbase, (uint32_t)(g * NCB * 2));
+    } else if constexpr (LUTM == kLutHalf) {
+      const int g = min(group_of(c0, a.g_magic), a.ng - 1);
+      lut_load_buf<BITS>(S.lr, rl, lbase + (uint32_t)(g * NCB * 2), 0u);
     }
   };
 
-  // running position in the row's staged entries (entries are sorted by column)
-  int p_run = 0;
-
-  auto store_step = [&](const StepRegs<BITS>& S, int kt, int buf, auto prep) __attribute__((always_inline)) {
-    constexpr bool kPrep = decltype(prep)::value;
-    const int k0 = kt * BK;
+  // A and W tiles of step kt into LDS buffer buf (outliers separately).
+  auto store_main = [&](const StepRegs<BITS>& S, int kt, int buf, auto even_c) __attribute__((always_inline)) {
+    constexpr bool kEven = decltype(even_c)::value;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int u = tid + NT * j;
-      const int row = u >> 3;
-      const int c8 = u & 7;
-      const bool ok = m0 + row < a.M && k0 + 8 * c8 < a.K;
-      const u32x4_t v = ok ? permute_p(S.x[j]) : u32x4_t{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4_t*>(&sm.a[buf][row * LDS_ROW + 8 * c8]) = v;
-    }
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(&sm.a[buf][xoff + 32 * j * BK]) = permute_p(S.x[j]);
     LutPlanes<BITS> pl;
-    if constexpr (PER_ROW) pl = pl_row;
-    else pl = lut_planes<BITS>(S.lr);
-    const int c16 = k0 + 16 * qq;
-    uint16_t* brow = &sm.b[buf][nl * LDS_ROW + 16 * qq];
-    {
-      uint32_t o[4];
-      dequant_piece16<BITS, 0>(S.cw, c16, pl, o);
-      *reinterpret_cast<u32x4_t*>(brow) = u32x4_t{o[0], o[1], o[2], o[3]};
-      dequant_piece16<BITS, 1>(S.cw, c16, pl, o);
-      *reinterpret_cast<u32x4_t*>(brow + 8) = u32x4_t{o[0], o[1], o[2], o[3]};
+    if constexpr (LUTM == kLutRow) {
+      pl = pl_row;
+    } else if constexpr (LUTM == kLutPair) {
+      if constexpr (kEven) pl_pair = lut_planes<BITS>(S.lr);
+      pl = pl_pair;
+    } else {
+      pl = lut_planes<BITS>(S.lr);
     }
-    if constexpr (HAS_CSR) {
-      const int ck = k0 / a.chunk;
-      const int cb = ck & 1;
-      const int kin = k0 - ck * a.chunk;     // step start inside the chunk
-      const int lo = kin + 16 * qq;          // my 16 columns inside the chunk
-      if (brow_ok) {
-        if constexpr (kPrep) {
-          if (kin == 0) p_run = sm.pos[cb][nl];
-          const int pend = sm.pos[cb][nl + 1];
-          while (p_run < pend) {
-            const uint32_t e = sm.ent[cb][p_run];
-            const int col = (int)(e & 0xFFFFu);
-            if (col >= lo + 16) break;
-            if (col >= lo) {
-              const int cs = col - lo;
-              brow[8 * (cs >> 3) + p_slot(cs & 7)] = (uint16_t)((e >> 16) << 8);
-            }
-            ++p_run;
+    const int c0 = kt * BK + 32 * hh;
+    uint16_t* brow = &sm.b[buf][nl * BK];
+    static_for<0, 4>([&](auto u_c) __attribute__((always_inline)) {
+      constexpr int U = decltype(u_c)::value;
+      uint32_t o[4];
+      dequant_unit<BITS, U>(S.cw, c0, pl, o);
+      *reinterpret_cast<u32x4_t*>(brow + 8 * ((4 * hh + U) ^ wsw)) = u32x4_t{o[0], o[1], o[2], o[3]};
+    });
+  };
+
+  // running position in the row's staged entries (entries are sorted by column)
+  // Walk over the row's staged entries (sorted by column): p_run indexes the entry in
+  // e0, e1 holds the one after (entries past the row's end read as column 0xFFFF), so
+  // a step's test needs no LDS round trip; an entry taken is refilled two ahead.
+  int p_run = 0, p_end = 0;
+  uint32_t e0 = ~0u, e1 = ~0u;
+
+  // Outliers of step (chunk ck, KIN columns into it) overwritten into the W tile in buf.
+  auto store_outliers = [&](int ck, int buf, auto kin_c, auto prep) __attribute__((always_inline)) {
+    constexpr int KIN = decltype(kin_c)::value;
+    constexpr bool kPrep = decltype(prep)::value;
+    const int cb = ck & 1;
+    const int lo = KIN + 32 * hh;  // my 32 columns inside the chunk
+    uint16_t* brow = &sm.b[buf][nl * BK];
+    if (brow_ok) {
+      if constexpr (kPrep) {
+        const uint32_t* ent = sm.ent[cb];
+        if constexpr (KIN == 0) {
+          p_run = sm.pos[cb][nl];
+          p_end = sm.pos[cb][nl + 1];
+          const uint32_t v0 = ent[min(p_run, kEntCap - 1)], v1 = ent[min(p_run + 1, kEntCap - 1)];
+          e0 = p_run < p_end ? v0 : ~0u;
+          e1 = p_run + 1 < p_end ? v1 : ~0u;
+        }
+        while ((int)(e0 & 0xFFFFu) < lo + 32) {
+          const int col = (int)(e0 & 0xFFFFu);
+          if (col >= lo) {
+            const int cs = col - lo;  // column inside my 32
+            brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + p_slot(cs & 7)] = (uint16_t)((e0 >> 16) << 8);
           }
-        } else {  // no prepared list (or a chunk beyond its capacity): read the row's chunk directly
-          const int32_t* offr = a.offsets + (size_t)nb * (a.nch + 1);
-          const int s1 = offr[ck + 1];
-          for (int e = offr[ck]; e < s1; ++e) {
-            const int cs = (int)a.cols[e] - lo;
-            if (cs >= 0 && cs < 16) brow[8 * (cs >> 3) + p_slot(cs & 7)] = (uint16_t)((uint32_t)a.vals[e] << 8);
+          ++p_run;
+          const uint32_t v = ent[min(p_run + 1, kEntCap - 1)];
+          e0 = e1;
+          e1 = p_run + 1 < p_end ? v : ~0u;
+        }
+      } else {  // no prepared list (or a chunk beyond its capacity): read the row's chunk directly
+        const int32_t* offr = a.offsets + (size_t)nb * (a.nch + 1);
+        const int s1 = offr[ck + 1];
+        for (int e = offr[ck]; e < s1; ++e) {
+          const int col = (int)a.cols[e];
+          if (col >= lo && col < lo + 32) {
+            const int cs = col - lo;
+            brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + p_slot(cs & 7)] = (uint16_t)((uint32_t)a.vals[e] << 8);
           }
         }
       }
@@ -279,178 +512,75 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   };
 
   // Prepared outlier entries of a chunk (slot of this N tile): loaded into registers
-  // two iterations before the chunk's first step is staged, written to ent/pos[ck & 1]
-  // at the end of the next iteration (after that iteration's readers of the other buffer).
-  u32x4_t ent_r = {0u, 0u, 0u, 0u}, pos_r = {0u, 0u, 0u, 0u};
+  // at the first step of the previous chunk, written to ent/pos[ck & 1] two steps
+  // before the chunk's first step is staged (after every reader of that buffer).
+  u32x4_t ent_r[2], pos_r;
   auto ent_load = [&](int ck) __attribute__((always_inline)) {
     const uint32_t* slot = a.tent + ((size_t)tn * a.nch + ck) * kSlotWords;
-    ent_r = *reinterpret_cast<const u32x4_t*>(slot + kPosWords + 4 * tid);
-    pos_r = *reinterpret_cast<const u32x4_t*>(slot + 4 * min(tid, kPosWords / 4 - 1));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      ent_r[h] = *reinterpret_cast<const u32x4_t*>(slot + kPosWords + 4 * (ptid + NP * h));
+    pos_r = *reinterpret_cast<const u32x4_t*>(slot + 4 * min(ptid, kPosWords / 4 - 1));
   };
   auto ent_store = [&](int ck) __attribute__((always_inline)) {
     const int cb = ck & 1;
-    *reinterpret_cast<u32x4_t*>(&sm.ent[cb][4 * tid]) = ent_r;
-    if (tid < kPosWords / 4) *reinterpret_cast<u32x4_t*>(&sm.pos[cb][4 * tid]) = pos_r;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) *reinterpret_cast<u32x4_t*>(&sm.ent[cb][4 * (ptid + NP * h)]) = ent_r[h];
+    if (ptid < kPosWords / 4) *reinterpret_cast<u32x4_t*>(&sm.pos[cb][4 * ptid]) = pos_r;
   };
 
-  float4_t acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-  auto mfma_step = [&](int buf) __attribute__((always_inline)) {
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      u32x4_t af[4], bf[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const u32x4_t*>(&sm.a[buf][(64 * wm + 16 * i + r) * LDS_ROW + 32 * ks + 8 * kq]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bf[j] = *reinterpret_cast<const u32x4_t*>(&sm.b[buf][(64 * wn + 16 * j + r) * LDS_ROW + 32 * ks + 8 * kq]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
-    }
-  };
-
-  // Prepared outlier lists are used when every chunk of this block's range fits its
-  // slot; otherwise the block reads the CSR arrays directly (a separate loop, so the
-  // hot loop carries no data-dependent loads).
-  __shared__ int s_direct;
-  const int ck_begin = (kt_begin * BK) / a.chunk;
-  const int ck_end = (max(kt_end, kt_begin + 1) * BK + a.chunk - 1) / a.chunk;
-  bool prepared = false;
-  if constexpr (HAS_CSR) {
-    if (a.tent != nullptr) {
-      if (tid == 0) s_direct = 0;
-      __syncthreads();
-      if (tid < ck_end - ck_begin &&
-          (int)a.tent[((size_t)tn * a.nch + ck_begin + tid) * kSlotWords + BN] > kEntCap)
-        s_direct = 1;
-      __syncthreads();
-      prepared = s_direct == 0;
-    }
-  }
-
+  // Register sets: DIST steps of loads in flight (the sets rotate by step index; even
+  // DIST keeps a set's step parity fixed, which the two-step group LUTs rely on).
+  constexpr int DIST = (SPC % 4 == 0) ? 4 : 2;
   auto run = [&](auto prep) __attribute__((always_inline)) {
     constexpr bool kPrep = decltype(prep)::value;
-    StepRegs<BITS> s0, s1;
-    if constexpr (kPrep) ent_load(ck_begin);
-    load_step(s0, kt_begin);
-    load_step(s1, min(kt_begin + 1, kt_last));
-    if constexpr (kPrep) {
+    StepRegs<BITS> rs[DIST];  // set d holds steps of index d (mod DIST) from the range start
+    if constexpr (HAS_CSR && kPrep) ent_load(ck_begin);
+    static_for<0, DIST>([&](auto d_c) __attribute__((always_inline)) {
+      constexpr int d = decltype(d_c)::value;
+      load_step(rs[d], kt_begin + d, std::integral_constant<bool, d % 2 == 0>{});
+    });
+    if constexpr (HAS_CSR && kPrep) {
       ent_store(ck_begin);
       __syncthreads();
-      p_run = sm.pos[ck_begin & 1][nl];
     }
-    store_step(s0, kt_begin, 0, prep);
-    if constexpr (kPrep) ent_load((min(kt_begin + 2, kt_last) * BK) / a.chunk);
+    store_main(rs[0], kt_begin, 0, std::integral_constant<bool, true>{});
+    if constexpr (HAS_CSR) store_outliers(ck_begin, 0, std::integral_constant<int, 0>{}, prep);
     // drain the prologue's loads once: the loop then starts from the same wait state as
     // its back edge, and the compiler does not add first-iteration waits to every trip
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained (gfx9 encoding)
     __syncthreads();
 
-    // One K step: loads of step kt+2 (clamped), MFMAs of step kt, LDS stores of step
-    // kt+1, the entries of step kt+2's chunk stored when it starts a chunk, the entries
-    // of step kt+3's chunk loaded (every step, so the wait counts never depend on data),
-    // barrier.
-    auto iter = [&](int kt, StepRegs<BITS>& sload, const StepRegs<BITS>& sstore) __attribute__((always_inline)) {
-      const int buf = (kt - kt_begin) & 1;
-      load_step(sload, min(kt + 2, kt_last));
-      // keep the loads ahead of the MFMAs: the scheduler would otherwise sink them
-      // past the matrix work (shrinking the prefetch distance to nothing)
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_step(buf);
-      // unconditional (the last trip stores a duplicate of the last step into the idle
-      // buffer) so that every trip leaves the same loads pending
-      store_step(sstore, min(kt + 1, kt_last), buf ^ 1, prep);
-      if constexpr (kPrep) {
-        const int k2 = (kt + 2) * BK;
-        if (kt + 2 < kt_end && k2 % a.chunk == 0) ent_store(k2 / a.chunk);
-        ent_load((min(kt + 3, kt_last) * BK) / a.chunk);
-      }
-      __syncthreads();
-    };
-    int kt = kt_begin;
-    for (; kt + 1 < kt_end; kt += 2) {  // two steps per trip: the register sets alternate
-      iter(kt, s0, s1);
-      iter(kt + 1, s1, s0);
+    // One chunk per trip, its SPC steps unrolled.  Step s (the consumers run the MFMAs
+    // of step kt meanwhile): loads of step kt+DIST, LDS stores of step kt+1 into the
+    // other buffer, barrier.
+    for (int c = ck_begin; c < ck_end; ++c) {
+      const int kb = c * SPC;
+      static_for<0, SPC>([&](auto s_c) __attribute__((always_inline)) {
+        constexpr int s = decltype(s_c)::value;
+        constexpr int buf = s & 1;
+        const int kt = kb + s;
+        load_step(rs[s % DIST], kt + DIST, std::integral_constant<bool, s % 2 == 0>{});
+        // keep the loads ahead of the stores of the other sets
+        __builtin_amdgcn_sched_barrier(0);
+        store_main(rs[(s + 1) % DIST], kt + 1, buf ^ 1, std::integral_constant<bool, (s + 1) % 2 == 0>{});
+        if constexpr (HAS_CSR) {
+          constexpr int KIN = ((s + 1) % SPC) * BK;
+          if (s + 1 < SPC || c + 1 < ck_end)
+            store_outliers(s + 1 < SPC ? c : c + 1, buf ^ 1, std::integral_constant<int, KIN>{}, prep);
+          if constexpr (kPrep) {
+            if constexpr (s == 0) ent_load(min(c + 1, ck_end - 1));
+            if constexpr (s == SPC - 2) ent_store(c + 1);
+          }
+        }
+        __syncthreads();
+      });
     }
-    if (kt < kt_end) iter(kt, s0, s1);
   };
-  if (kt_begin < kt_end) {
-    if (prepared)
-      run(std::integral_constant<bool, true>{});
-    else
-      run(std::integral_constant<bool, false>{});
-  }
-
-  // Epilogue.  Lane holds D[4*kq + e][r] of every 16x16 tile (i, j).
-  if (a.splits == 1) {
-    if (a.r > 0) {
-      // acc += s * H . B^T on the matrix core in fp32 (V_MFMA_F32_16X16X4_F32: A = s*H,
-      // lane l holds row l%16, k = l/16; B = B^T, lane l holds k = l/16, column l%16).
-      // Sixteen rank columns per round, their loads issued together (clamped, zero-selected).
-      for (int kr = 0; kr < a.r; kr += 16) {
-        float hv[4][4], bv[4][4];
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const int k = kr + 4 * kk + kq;
-          const int kc = min(k, a.r - 1);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int ma = m0 + 64 * wm + 16 * i + r;
-            const float h = a.H[(size_t)min(ma, a.M - 1) * a.r + kc];
-            hv[i][kk] = (ma < a.M && k < a.r) ? a.scale * h : 0.f;
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int n = n0 + 64 * wn + 16 * j + r;
-            const float b = h2f(a.B[(size_t)min(n, a.N - 1) * a.r + kc]);
-            bv[j][kk] = (n < a.N && k < a.r) ? b : 0.f;
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[i][kk], bv[j][kk], acc[i][j], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + 64 * wn + 16 * j + r;
-      if (n >= a.N) continue;
-      const float g = a.r > 0 ? h2f(a.gamma[n]) : 1.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = m0 + 64 * wm + 16 * i + 4 * kq + e;
-          if (m < a.M) a.out[(size_t)m * a.N + n] = f2h_rn(a.r > 0 ? acc[i][j][e] * g : acc[i][j][e]);
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = n0 + 64 * wn + 16 * j + r;
-        if (n >= a.N) continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = m0 + 64 * wm + 16 * i + 4 * kq + e;
-          if (m < a.M) a.partial[((size_t)split * a.M + m) * a.N + n] = acc[i][j][e];
-        }
-      }
-    }
-  }
+  if (prepared)
+    run(std::integral_constant<bool, true>{});
+  else
+    run(std::integral_constant<bool, false>{});
 }
 
 // Prepared outlier entries: one slot per (N tile, chunk) with the row prefix of the
@@ -461,7 +591,7 @@ __global__ __launch_bounds__(BN) void tile_entries_kernel(const int32_t* __restr
                                                           const uint16_t* __restrict__ cols,
                                                           const uint8_t* __restrict__ vals, int N, int nch,
                                                           uint32_t* __restrict__ tent) {
-  __shared__ int part[2];
+  __shared__ int part[BN / 64];
   const int tn = blockIdx.x / nch;
   const int ck = blockIdx.x - tn * nch;
   const int t = threadIdx.x;
@@ -472,7 +602,7 @@ __global__ __launch_bounds__(BN) void tile_entries_kernel(const int32_t* __restr
     o2 = offsets[(size_t)n * (nch + 1) + ck + 1];
   }
   const int cnt = o2 - o1;
-  int incl = cnt;  // inclusive prefix inside the wave, then across the two waves
+  int incl = cnt;  // inclusive prefix inside the wave, then across the waves
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
     const int u = __shfl_up(incl, d);
@@ -480,8 +610,12 @@ __global__ __launch_bounds__(BN) void tile_entries_kernel(const int32_t* __restr
   }
   if ((t & 63) == 63) part[t >> 6] = incl;
   __syncthreads();
-  if (t >= 64) incl += part[0];
-  const int total = part[0] + part[1];
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < BN / 64; ++w) {
+    if (w < (t >> 6)) incl += part[w];
+    total += part[w];
+  }
   uint32_t* slot = tent + (size_t)blockIdx.x * kSlotWords;
   slot[t] = (uint32_t)(incl - cnt);
   if (t < kPosWords - BN) slot[BN + t] = (uint32_t)total;
@@ -490,36 +624,50 @@ __global__ __launch_bounds__(BN) void tile_entries_kernel(const int32_t* __restr
       slot[kPosWords + incl - cnt + j] = (uint32_t)cols[o1 + j] | ((uint32_t)vals[o1 + j] << 16);
 }
 
-template <int BITS, bool PER_ROW, bool HAS_CSR, bool X_VEC>
+template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC>
 hipError_t launch_variant(const GemmArgs& a, dim3 grid, hipStream_t stream) {
-  auto* fn = gemm_kernel<BITS, PER_ROW, HAS_CSR, X_VEC>;
-  static bool attr_set = false;  // > 64 KiB of LDS must be requested once per kernel
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(GemmSmem));
+  auto* fn = gemm_kernel<BITS, LUTM, HAS_CSR, X_VEC>;
+  // > 64 KiB of LDS is requested once per kernel and device
+  static uint64_t attr_set = 0;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(__atomic_load_n(&attr_set, __ATOMIC_ACQUIRE) & bit)) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)sizeof(GemmSmem));
     if (e != hipSuccess) return e;
-    attr_set = true;
+    __atomic_fetch_or(&attr_set, bit, __ATOMIC_ACQ_REL);
   }
   hipLaunchKernelGGL(fn, grid, dim3(NT), sizeof(GemmSmem), stream, a);
   return hipGetLastError();
 }
 
-template <int BITS, bool X_VEC>
-hipError_t launch_bits(const GemmArgs& a, bool per_row, dim3 grid, hipStream_t stream) {
-  if (per_row)
-    return a.has_csr ? launch_variant<BITS, true, true, X_VEC>(a, grid, stream)
-                     : launch_variant<BITS, true, false, X_VEC>(a, grid, stream);
-  return a.has_csr ? launch_variant<BITS, false, true, X_VEC>(a, grid, stream)
-                   : launch_variant<BITS, false, false, X_VEC>(a, grid, stream);
+template <int BITS, int LUTM, bool X_VEC>
+hipError_t launch_csr(const GemmArgs& a, dim3 grid, hipStream_t stream) {
+  return a.has_csr ? launch_variant<BITS, LUTM, true, X_VEC>(a, grid, stream)
+                   : launch_variant<BITS, LUTM, false, X_VEC>(a, grid, stream);
 }
 
-template <bool X_VEC>
-hipError_t launch_any(const GemmArgs& a, int bits, bool per_row, dim3 grid, hipStream_t stream) {
+template <int BITS>
+hipError_t launch_bits(const GemmArgs& a, int lutm, bool x_vec, dim3 grid, hipStream_t stream) {
+  if (!x_vec)  // unaligned or ragged activations: generic loads, row or per-32-column group LUTs
+    return lutm == kLutRow ? launch_csr<BITS, kLutRow, false>(a, grid, stream)
+                           : launch_csr<BITS, kLutHalf, false>(a, grid, stream);
+  switch (lutm) {
+    case kLutRow: return launch_csr<BITS, kLutRow, true>(a, grid, stream);
+    case kLutPair: return launch_csr<BITS, kLutPair, true>(a, grid, stream);
+    case kLutStep: return launch_csr<BITS, kLutStep, true>(a, grid, stream);
+    default: return launch_csr<BITS, kLutHalf, true>(a, grid, stream);
+  }
+}
+
+hipError_t launch_any(const GemmArgs& a, int bits, int lutm, bool x_vec, dim3 grid, hipStream_t stream) {
   switch (bits) {
-    case 1: return launch_bits<1, X_VEC>(a, per_row, grid, stream);
-    case 2: return launch_bits<2, X_VEC>(a, per_row, grid, stream);
-    case 3: return launch_bits<3, X_VEC>(a, per_row, grid, stream);
-    default: return launch_bits<4, X_VEC>(a, per_row, grid, stream);
+    case 1: return launch_bits<1>(a, lutm, x_vec, grid, stream);
+    case 2: return launch_bits<2>(a, lutm, x_vec, grid, stream);
+    case 3: return launch_bits<3>(a, lutm, x_vec, grid, stream);
+    default: return launch_bits<4>(a, lutm, x_vec, grid, stream);
   }
 }
 
@@ -531,14 +679,16 @@ SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes)
   const int spc = std::max(1, L.chunk / BK);
   const int nchunks = (ksteps + spc - 1) / spc;
   const long tiles = (long)((L.N + BN - 1) / BN) * (long)((M + BM - 1) / BM);
-  const int target = std::max(1, cu_count);  // one 512-thread block per CU
+  const int target = std::max(1, cu_count);  // one 512-thread block per CU (LDS-bound)
   // prepared outlier entries, when the workspace holds them
   const size_t ent_bytes = (L.offsets != nullptr)
                                ? (size_t)((L.N + BN - 1) / BN) * (size_t)L.nch * kSlotWords * sizeof(uint32_t)
                                : 0;
   const size_t ent_room = workspace_bytes >= ent_bytes ? ent_bytes : 0;
   int splits = 1;
-  if (tiles < target) splits = (int)std::min<long>((target + tiles - 1) / tiles, kMaxSplits);
+  // Split K only while a whole extra round of tiles fits on the CUs: with one block per CU,
+  // tiles >= CUs/2 gain nothing from splitting (the rounds stay the same) and pay the reduce.
+  if (2 * tiles <= target) splits = (int)std::min<long>(target / tiles, kMaxSplits);
   splits = std::min(splits, nchunks);  // splits hold whole outlier chunks
   const size_t per_split = (size_t)M * (size_t)L.N * sizeof(float);
   while (splits > 1 && (size_t)splits * per_split + ent_room > workspace_bytes) --splits;
@@ -584,7 +734,13 @@ hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_
   a.tiles_m = (M + BM - 1) / BM;
   a.tiles_n = (L.N + BN - 1) / BN;
   a.tiles = a.tiles_m * a.tiles_n;
-  const bool x_vec = (reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (L.K % 8) == 0 && L.K >= 8;
+  // buffer offsets are 32-bit: activations, codes and LUTs stay below 2^31 bytes
+  const bool x_vec = (reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (L.K % 8) == 0 && L.K >= 8 &&
+                     ((size_t)M + BM) * (size_t)L.K * 2 < kOutOfRange;
+  if ((size_t)L.N * L.wpr * 4 >= kOutOfRange || (size_t)L.N * L.ng * ((size_t)2 << L.bits) >= kOutOfRange)
+    return hipErrorInvalidValue;
+  if (L.chunk != (L.bits == 3 ? 640 : 512)) return hipErrorInvalidValue;
+  if (L.group_size > 0 && L.ng > 1 && L.group_size % 32 != 0) return hipErrorInvalidValue;
   const size_t part_bytes = plan.splits > 1 ? (size_t)plan.splits * M * L.N * sizeof(float) : 0;
   a.tent = nullptr;
   if (a.has_csr && plan.aux_bytes > 0) {
@@ -595,11 +751,11 @@ hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_
     if (e != hipSuccess) return e;
   }
   const dim3 grid(a.tiles * plan.splits);
-  const bool per_row = L.group_size <= 0 || L.ng == 1;
-  const hipError_t err = x_vec ? launch_any<true>(a, L.bits, per_row, grid, stream)
-                               : launch_any<false>(a, L.bits, per_row, grid, stream);
+  const int G = L.group_size;
+  const int lutm = (G <= 0 || L.ng == 1) ? kLutRow : (G % 128 == 0) ? kLutPair : (G % 64 == 0) ? kLutStep : kLutHalf;
+  const hipError_t err = launch_any(a, L.bits, lutm, x_vec, grid, stream);
   if (err != hipSuccess) return err;
-  if (plan.splits > 1) return launch_splitk_reduce(workspace, plan.splits, M, L.N, D, out, stream);
+  if (plan.splits > 1) return launch_splitk_sum(workspace, plan.splits, M, L.N, out, stream);
   return hipSuccess;
 }
 

@@ -61,9 +61,8 @@ hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_
 
 hipError_t launch_dequant(const Layer& L, uint16_t* W, hipStream_t stream);
 
-// Sum of fp32 split-K partials [splits, M, N] followed by the DoRA epilogue.
-hipError_t launch_splitk_reduce(const float* partial, int splits, int M, int N, const Dora& D, uint16_t* out,
-                                hipStream_t stream);
+// out = fp16_rn(sum of fp32 split-K partials [splits, M, N]) (epilogue already applied).
+hipError_t launch_splitk_sum(const float* partial, int splits, int M, int N, uint16_t* out, hipStream_t stream);
 
 // Decode finish: sum split partials, round the DoRA H (from hpart partial sums
 // over h_blocks column blocks, or D.H) and apply the epilogue.
