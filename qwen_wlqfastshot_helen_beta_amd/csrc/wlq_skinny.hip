@@ -348,6 +348,41 @@ __device__ __forceinline__ void arrive_product(const SkinnyArgs& a, int rb, floa
 
 // DoRA block: hpart is written; count one arrival on every row block and finish,
 // in one parallel pass, the row blocks for which this block is the last.
+// One K split and the DoRA blocks already done (their arrivals fill the row block's count
+// but one): nobody else touches the row block in this call, so the block applies the
+// epilogue from its accumulators, without the partial round trip, and clears the count.
+// Returns false (nothing done) when the DoRA blocks are still running.
+template <int MT>
+__device__ __forceinline__ bool finish_direct(const SkinnyArgs& a, int rb, int n, bool row_ok, int kq,
+                                              const float4_t acc[MT], float* lds) {
+  __shared__ int s_ready;
+  __syncthreads();  // every wave is past its last use of the activation staging (reused below)
+  if (threadIdx.x == 0)
+    s_ready = __hip_atomic_load(a.sync + rb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(a.arrivals - 1);
+  __syncthreads();
+  if (!s_ready) return false;
+  fence_acquire();
+  for (int idx = threadIdx.x; idx < a.M * a.r; idx += blockDim.x)
+    lds[idx] = h2f(f2h_rn(sum_dev(a.hpart + idx, (size_t)a.M * a.r, a.h_blocks)));
+  __syncthreads();
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * mt + 4 * kq + e;
+      if (i < a.M && row_ok) {
+        float ls = 0.f;
+        const float* hi = lds + (size_t)i * a.r;
+        const uint16_t* bb = a.B + (size_t)n * a.r;
+        for (int j = 0; j < a.r; ++j) ls += hi[j] * h2f(bb[j]);
+        a.out[(size_t)i * a.N + n] = f2h_rn((acc[mt][e] + a.scale * ls) * h2f(a.gamma[n]));
+      }
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(a.sync + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 __device__ __forceinline__ void arrive_dora(const SkinnyArgs& a, float* lds) {
   __shared__ int s_list[256];
   __shared__ int s_n;
@@ -591,26 +626,32 @@ __device__ __forceinline__ void fast_block(const u32x4_t& codes, const LutPlanes
 }
 
 // Wave-private LDS tiles of one outlier chunk (4 slabs x 16 rows):
-//   ctile: code windows, [slab][kq][row] x 16 B
+//   ctile: code windows, [slab][row][window ^ ((row >> 2) & 3)] x 16 B
 //   ltile: LUT byte planes, [slab][group][lo|hi][row] x 16 B (the per-row LUT: [lo|hi][row])
-// Rows are the fastest index, so the 64 lanes of a wave write 64 consecutive words
-// or 16-byte chunks: no LDS bank conflicts on the per-slab stores and reads.
+// The code windows and LUT quarters are loaded with the four lanes of a row adjacent
+// (lane 4 * row + window: coalesced 64-byte and 32-byte row pieces) and exchanged
+// through these tiles to the MFMA lane order (lane row + 16 * window); the window
+// swizzle keeps both the stores and the reads free of LDS bank conflicts.
 template <int NGS>
 struct ChunkTiles {
   uint32_t* ctile;
   uint32_t* ltile;
 };
 
+// Dword offset of code window `w` of tile row `row` in slab `sl` of a ctile.
+__device__ __forceinline__ int ctile_word(int sl, int row, int w) { return ((sl * 16 + row) * 4 + (w ^ ((row >> 2) & 3))) * 4; }
+
+// s was loaded by lane (rl, kl) = (lane / 4, lane % 4); the MFMA lane is (r, kq).
 template <bool PER_ROW, int NGS, int MT>
 __device__ __forceinline__ void stage4_consume(const Stage4<NGS>& s, int slab_in_chunk, LutPlanes<4>& pl,
-                                               const ChunkTiles<NGS>& tl, int r, int kq,
+                                               const ChunkTiles<NGS>& tl, int r, int kq, int rl, int kl,
                                                const uint16_t* const xp[MT], float4_t acc[MT]) {
-  *reinterpret_cast<u32x4_t*>(tl.ctile + ((slab_in_chunk * 4 + kq) * 16 + r) * 4) = s.codes;
+  *reinterpret_cast<u32x4_t*>(tl.ctile + ctile_word(slab_in_chunk, rl, kl)) = s.codes;
   if constexpr (!PER_ROW) {
-    // split my LUT quarters into planes and exchange them with the row's other lanes
+    // split the loaded LUT quarters into planes; the row's lanes exchange them
 #pragma unroll
     for (int j = 0; j < NGS; ++j) {
-      uint32_t* base = tl.ltile + ((slab_in_chunk * NGS + j) * 2 * 16 + r) * 4 + kq;
+      uint32_t* base = tl.ltile + ((slab_in_chunk * NGS + j) * 2 * 16 + rl) * 4 + kl;
       base[0] = perm_b32(s.lq[j].y, s.lq[j].x, 0x06040200u);
       base[16 * 4] = perm_b32(s.lq[j].y, s.lq[j].x, 0x07050301u);
     }
@@ -621,10 +662,11 @@ __device__ __forceinline__ void stage4_consume(const Stage4<NGS>& s, int slab_in
     pl.lo[0] = lo.x; pl.lo[1] = lo.y; pl.lo[2] = lo.z; pl.lo[3] = lo.w;
     pl.hi[0] = hi.x; pl.hi[1] = hi.y; pl.hi[2] = hi.z; pl.hi[3] = hi.w;
   }
-  fast_block<MT, 0>(s.codes, pl, xp, acc);
-  fast_block<MT, 1>(s.codes, pl, xp, acc);
-  fast_block<MT, 2>(s.codes, pl, xp, acc);
-  fast_block<MT, 3>(s.codes, pl, xp, acc);
+  const u32x4_t codes = *reinterpret_cast<const u32x4_t*>(tl.ctile + ctile_word(slab_in_chunk, r, kq));
+  fast_block<MT, 0>(codes, pl, xp, acc);
+  fast_block<MT, 1>(codes, pl, xp, acc);
+  fast_block<MT, 2>(codes, pl, xp, acc);
+  fast_block<MT, 3>(codes, pl, xp, acc);
 }
 
 // CSR entries of one chunk for one lane: entries e0 + kq + 4j, j < kEB.  The
@@ -660,7 +702,7 @@ __device__ __forceinline__ void entry_delta(const SkinnyArgs& a, const ChunkTile
   const int gcol = c * 512 + cl;
   if (gcol < k_lo || gcol >= k_hi) return;
   const int sl = cl >> 7;
-  const uint32_t word = tl.ctile[((sl * 4 + ((cl >> 5) & 3)) * 16 + r) * 4 + ((cl >> 3) & 3)];
+  const uint32_t word = tl.ctile[ctile_word(sl, r, (cl >> 5) & 3) + ((cl >> 3) & 3)];
   const uint32_t code = (word >> (4 * (cl & 7))) & 15u;
   const int gi = PER_ROW ? 0 : (NGS == 1 ? 0 : (NGS == 2 ? ((cl >> 6) & 1) : ((cl >> 5) & 3)));
   const unsigned char* planes =
@@ -720,8 +762,13 @@ __global__ __launch_bounds__(256, (NGS >= 4 || MT > 1 || (MB > 4 && NGS > 1)) ? 
   const int n = rb * kRowsPerBlock + wave * 16 + r;
   const bool row_ok = n < a.N;
   const int nc = row_ok ? n : (a.N - 1);
-  const uint32_t* qrow = a.q + (size_t)nc * a.wpr;
   const uint16_t* lrow = a.lut + (size_t)nc * a.ng * 16;
+  // loads: lane (rl, kl) takes window kl of tile row rl (the row's four lanes adjacent)
+  const int rl = lane >> 2;
+  const int kl = lane & 3;
+  const int nload = min(rb * kRowsPerBlock + wave * 16 + rl, a.N - 1);
+  const uint32_t* qrow_ld = a.q + (size_t)nload * a.wpr;
+  const uint16_t* lrow_ld = a.lut + (size_t)nload * a.ng * 16;
 
   const size_t xbytes = ((size_t)a.M * a.xstride * 2 + 15) & ~(size_t)15;
   uint16_t* zpad = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(smem) + xbytes);
@@ -772,7 +819,7 @@ __global__ __launch_bounds__(256, (NGS >= 4 || MT > 1 || (MB > 4 && NGS > 1)) ? 
   const int t_last = max(t_end - 1, t_begin);
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    stage4_load<PER_ROW, NGS>(st[j], a, qrow, lrow, kq, min(max(4 * c_begin + j, t_begin), t_last));
+    stage4_load<PER_ROW, NGS>(st[j], a, qrow_ld, lrow_ld, kl, min(max(4 * c_begin + j, t_begin), t_last));
 #pragma unroll
   for (int jj = 0; jj < (kOT + 3) / 4; ++jj) otile[min(kq + 4 * jj, nchunks)] = offv[jj];
   if (xfast)
@@ -816,9 +863,9 @@ __global__ __launch_bounds__(256, (NGS >= 4 || MT > 1 || (MB > 4 && NGS > 1)) ? 
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           xp[mt] = (16 * mt + r < a.M) ? xs + (16 * mt + r) * a.xstride + (t - seg0) * SLAB + kq * 32 : zpad;
-        stage4_consume<PER_ROW, NGS, MT>(st[s], s, pl, tl, r, kq, xp, acc);
+        stage4_consume<PER_ROW, NGS, MT>(st[s], s, pl, tl, r, kq, rl, kl, xp, acc);
       }
-      if constexpr (kMore) stage4_load<PER_ROW, NGS>(st[s], a, qrow, lrow, kq, min(t + 4, t_last));
+      if constexpr (kMore) stage4_load<PER_ROW, NGS>(st[s], a, qrow_ld, lrow_ld, kl, min(t + 4, t_last));
     }
     if (csr && row_ok) chunk_outliers<MB, PER_ROW, NGS>(a, cur, tl, xs, r, kq, c, k_lo, k_hi, seg0 * SLAB, corr);
   };
@@ -876,6 +923,9 @@ __global__ __launch_bounds__(256, (NGS >= 4 || MT > 1 || (MB > 4 && NGS > 1)) ? 
       }
     }
   }
+  if (a.sync && a.splits == 1 && a.h_blocks > 0 &&
+      finish_direct<MT>(a, rb, n, row_ok, kq, acc, reinterpret_cast<float*>(smem)))
+    return;
   write_result<MT>(a, split, n, row_ok, kq, acc);
   if (a.sync) {
     __syncthreads();
