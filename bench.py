@@ -176,12 +176,50 @@ def run_single_op(args) -> int:
     return 0
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def box_peaks(dev):
+    """Reference points measured on this GPU: torch's dense fp16 GEMM (hipBLASLt) on the
+    gate shape at M = 2048 with random data, and a 512 MiB device copy."""
+    import torch
+
+    M, N, K = 2048, 18944, 3584
+    a = torch.randn(M, K, device=dev).half()
+    bt = torch.randn(K, N, device=dev).half()  # W^T stored contiguous: a plain NN product
+    c = torch.empty(M, N, device=dev, dtype=torch.float16)
+    g = graph_of([lambda: torch.mm(a, bt, out=c)])
+    time_graph(g, 3)
+    ms = time_graph(g, 10)
+    tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    gc = graph_of([lambda: dst.copy_(src)])
+    time_graph(gc, 3)
+    msc = time_graph(gc, 10)
+    copy_gbs = 2 * src.numel() / (msc * 1e-3) / 1e9  # read + write
+    props = torch.cuda.get_device_properties(dev)
+    del a, bt, c, src, dst, g, gc
+    log(f"[bench] box: torch fp16 GEMM {tf:.0f} TFLOP/s, device copy {copy_gbs:.0f} GB/s (read+write)")
+    return {"torch_fp16_gemm_gate_m2048_TFLOP/s": round(tf, 1),
+            "device_copy_GB/s_read_plus_write": round(copy_gbs, 1),
+            "device": props.name, "compute_units": props.multi_processor_count}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--sweep", action="store_true", help="also time M in {4, 8, 16, 32} per shape")
+    ap.add_argument("--no-sweep", action="store_true", help="skip M in {4, 8, 16, 32} per shape (config 1)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the M=2048 GEMM leg")
     ap.add_argument("--op", default=None,
@@ -246,7 +284,7 @@ def main() -> int:
         return ms
 
     per_shape = {}
-    Ms = [1, 4, 8, 16, 32] if args.sweep else [1]
+    Ms = [1] if args.no_sweep else [1, 4, 8, 16, 32]
     shapes = dict(layers)
     shapes["gate_up_proj"] = merged["gate_up_proj"]
     for n, L in shapes.items():
@@ -265,9 +303,21 @@ def main() -> int:
                           "gate_up_proj 37888x3584 M=1",
                 "bytes_per_launch": merged["gate_up_proj"].headline_bytes(), "avg_us": dom["us"]}
 
-    # ---- prefill GEMM, M = 2048 (config 2)
-    gemm = None
+    # ---- prefill GEMM, M = 128 (config 2, the ridge: both fractions) and M = 2048
+    gemm = gemm128 = None
     if not args.no_gemm:
+        rows128 = {}
+        for n in names:
+            L = layers[n]
+            ms = op_time(L, 128, reps=5)
+            fl = 2.0 * 128 * L.N * L.K
+            tf = fl / (ms * 1e-3) / 1e12
+            gbs = L.headline_bytes() / (ms * 1e-3) / 1e9
+            rows128[n] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                          "frac_mfma": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "GB/s": round(gbs, 1),
+                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+            log(f"[bench] gemm {n:9s} M=128: {ms * 1e3:8.1f} us  {tf:7.1f} TFLOP/s  {gbs:7.0f} GB/s")
+        gemm128 = {"M": 128, "per_shape": rows128}
         M = 2048
         tot_flop, tot_ms, rows = 0.0, 0.0, {}
         for n in names:
@@ -282,6 +332,10 @@ def main() -> int:
         gemm = {"M": M, "TFLOP/s": round(tf, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
                 "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "per_shape": rows}
 
+    # ---- what this box sustains on plain work: a dense fp16 GEMM through torch (hipBLASLt)
+    # at the gate shape and M = 2048, and a device-to-device copy of 512 MiB
+    box = box_peaks(dev) if not args.no_gemm else None
+
     # ---- cpu_baseline: the reference's CPU dequant+matmul path on this host
     cpu = None
     if not args.no_cpu:
@@ -293,7 +347,7 @@ def main() -> int:
         xk = {K: x.cpu() for K, x in xs.items()}
         t_full, t_cached = cpu_path.time_layers(cl, xk, reps=5)
         cpu = {"value": round(step_bytes / t_full / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-               "kind": "port",
+               "kind": "port", "cpu_model": cpu_model(),
                "sample": "the 7 projections at M=1, dequant+matmul per call as the reference's CPU path does "
                          f"(median of 5 passes, {t_full:.2f} s/pass); matmul-only with cached W0 {t_cached:.3f} s/pass",
                "matmul_only_GB/s": round(step_bytes / t_cached / 1e9, 3)}
@@ -321,6 +375,8 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "gemm_m2048": gemm,
+        "gemm_m128": gemm128,
+        "box_peaks": box,
         "per_shape": per_shape,
     }
     print(json.dumps(out), flush=True)
