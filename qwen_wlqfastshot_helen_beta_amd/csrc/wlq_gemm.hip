@@ -11,8 +11,8 @@
 //   V_MFMA_F32_16X16X32_F16 (accumulators in AGPRs): per K step they read the
 //   step's fragments from LDS and issue 64 MFMAs each, nothing else.
 // * 4 producer waves (one per SIMD) fill the other LDS buffer with the next
-//   step meanwhile: activations permuted to column order P, codes expanded
-//   through their LUT byte planes (two threads per W row, 32 columns each),
+//   step meanwhile: activations as they are, codes expanded through their LUT
+//   byte planes into natural column order (two threads per W row, 32 columns each),
 //   outliers overwritten (the reference's W0 = e5m2 << 8 at outlier positions).
 //   Their global loads run four steps ahead in registers (two for 3-bit).
 //
@@ -152,11 +152,17 @@ __device__ __forceinline__ void lut_load_buf(LutRaw<BITS>& raw, __amdgpu_buffer_
   }
 }
 
-// 8 columns (unit U of the thread's 32, columns c0 + 8U ..) expanded to fp16 pairs in order P.
+// 8 columns (unit U of the thread's 32, columns c0 + 8U ..) expanded to fp16 pairs in
+// natural column order (the activations are then staged as they are in memory).
 template <int BITS, int U>
 __device__ __forceinline__ void dequant_unit(const uint32_t* w, int c0, const LutPlanes<BITS>& t, uint32_t out[4]) {
   if constexpr (BITS == 4) {
-    dequant_word4(w[U], t, out);
+    uint32_t p[4];  // order P: (c0,c2) (c4,c6) (c1,c3) (c5,c7)
+    dequant_word4(w[U], t, p);
+    out[0] = perm_b32(p[2], p[0], 0x05040100u);  // (c0, c1)
+    out[1] = perm_b32(p[2], p[0], 0x07060302u);  // (c2, c3)
+    out[2] = perm_b32(p[3], p[1], 0x05040100u);  // (c4, c5)
+    out[3] = perm_b32(p[3], p[1], 0x07060302u);  // (c6, c7)
   } else {
     constexpr int P = U >> 1;    // 16-column piece
     constexpr int BLK = U & 1;   // 8-column block inside the piece
@@ -183,9 +189,10 @@ __device__ __forceinline__ void dequant_unit(const uint32_t* w, int c0, const Lu
         code[j] = (uint32_t)(src >> sh) & 7u;
       }
     }
-    const uint32_t se = code[0] | (code[2] << 8) | (code[4] << 16) | (code[6] << 24);
-    const uint32_t so = code[1] | (code[3] << 8) | (code[5] << 16) | (code[7] << 24);
-    dequant_sel8<BITS>(se, so, t, out);
+    // selectors of columns 0-3 and 4-7: the lookups then come out in natural order
+    const uint32_t s0 = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+    const uint32_t s1 = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+    dequant_sel8<BITS>(s0, s1, t, out);
   }
 }
 
@@ -442,7 +449,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   auto store_main = [&](const StepRegs<BITS>& S, int kt, int buf, auto even_c) __attribute__((always_inline)) {
     constexpr bool kEven = decltype(even_c)::value;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(&sm.a[buf][xoff + 32 * j * BK]) = permute_p(S.x[j]);
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(&sm.a[buf][xoff + 32 * j * BK]) = S.x[j];
     LutPlanes<BITS> pl;
     if constexpr (LUTM == kLutRow) {
       pl = pl_row;
@@ -490,7 +497,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
           const int col = (int)(e0 & 0xFFFFu);
           if (col >= lo) {
             const int cs = col - lo;  // column inside my 32
-            brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + p_slot(cs & 7)] = (uint16_t)((e0 >> 16) << 8);
+            brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + (cs & 7)] = (uint16_t)((e0 >> 16) << 8);
           }
           ++p_run;
           const uint32_t v = ent[min(p_run + 1, kEntCap - 1)];
@@ -504,7 +511,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
           const int col = (int)a.cols[e];
           if (col >= lo && col < lo + 32) {
             const int cs = col - lo;
-            brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + p_slot(cs & 7)] = (uint16_t)((uint32_t)a.vals[e] << 8);
+            brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + (cs & 7)] = (uint16_t)((uint32_t)a.vals[e] << 8);
           }
         }
       }

@@ -1003,7 +1003,10 @@ SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_byte
   splits = (total + sps - 1) / sps;
   p.splits = splits;
   p.slabs_per_split = sps;
-  const int seg_cols_max = kXStageBytes / (2 * std::max(1, M));
+  // activation staging: for M >= 8 a smaller budget (more restaging, less LDS per block)
+  // keeps two blocks per CU resident (measured: gate_proj at M = 8 41.0 -> 32.7 us)
+  const int x_budget = M >= 8 ? kXStageBytes / 2 : kXStageBytes;
+  const int seg_cols_max = x_budget / (2 * std::max(1, M));
   int seg = std::max(1, std::min(sps, (seg_cols_max - 8) / slab));
   if (L.bits == 4 && seg < sps) seg = std::max(kPF, seg / kPF * kPF);
   p.seg_slabs = seg;
