@@ -130,11 +130,11 @@ def op_fn(m, L, x, out):
         if M == 1:
             torch.ops.wlq_fastShot.gemv(m.q_packed_aligned, m.lut_c, x[0], out[0], L.N, L.K, 4, m.chunk_offsets,
                                         m.chunk_cols, m.chunk_vals, m.lora_B, None, m.dora_gamma, 1.0, 128,
-                                        m.lora_A_f16)
+                                        m.lora_A_f16, m.wlq_prepared)
         else:
             torch.ops.wlq_fastShot.gemm(x, m.q_packed_aligned, m.lut_c, out, L.N, L.K, 4, L.wpr, m.chunk_offsets,
                                         m.chunk_cols, m.chunk_vals, None, m.lora_B, m.dora_gamma, 1.0, 128,
-                                        m.lora_A_f16)
+                                        m.lora_A_f16, m.wlq_prepared)
     return fn
 
 
@@ -163,7 +163,7 @@ def run_single_op(args) -> int:
     layers, merged = build_layers(dev, want)
     L = merged.get(args.op) or layers[args.op]
     copies = max(2, math.ceil(512e6 / L.headline_bytes()) + 1)
-    mods = [attach_synthetic(torch.nn.Module(), L, dev) for _ in range(copies)]
+    mods = [attach_synthetic(torch.nn.Module(), L, dev, prepared=not args.row_layout) for _ in range(copies)]
     vw.init_workspaces(L.N, L.K, dev)
     x = torch.randn(args.M, L.K, device=dev).half()
     out = torch.empty(args.M, L.N, device=dev, dtype=torch.float16)
@@ -225,6 +225,8 @@ def main() -> int:
     ap.add_argument("--op", default=None,
                     help="only repeat this product (e.g. gate_up_proj) or 'copy' (256 MiB device copy), for profiling")
     ap.add_argument("--M", type=int, default=1)
+    ap.add_argument("--row-layout", action="store_true",
+                    help="run the decode products on the reference row-aligned layout (no prepared layout)")
     ap.add_argument("--reps", type=int, default=50)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -252,7 +254,9 @@ def main() -> int:
     copies = max(8, math.ceil(512e6 / step_bytes) + 1)
     method = WLQLinearMethod(vw.WLQFastShotConfig(bits=4, group_size=128))
     vnames = list(merged)
-    vmods = [{n: attach_synthetic(torch.nn.Module(), merged[n], dev) for n in vnames} for _ in range(copies)]
+    prep = not args.row_layout
+    vmods = [{n: attach_synthetic(torch.nn.Module(), merged[n], dev, prepared=prep) for n in vnames}
+             for _ in range(copies)]
     vw.init_workspaces(max(L.N for L in merged.values()), max(L.K for L in merged.values()), dev)
     xs = {K: torch.randn(1, K, device=dev).half() for K in {L.K for L in layers.values()}}
     log(f"[bench] {copies} weight copies (layers), {copies * step_bytes / 1e6:.0f} MB resident")
@@ -274,7 +278,7 @@ def main() -> int:
 
     # ---- per-shape products: `copies` launches of one product in one graph
     def op_time(L, M, reps=20):
-        mods = [attach_synthetic(torch.nn.Module(), L, dev) for _ in range(copies)]
+        mods = [attach_synthetic(torch.nn.Module(), L, dev, prepared=prep) for _ in range(copies)]
         xm = torch.randn(M, L.K, device=dev).half()
         out = torch.empty(M, L.N, device=dev, dtype=torch.float16)
         g = graph_of([op_fn(m, L, xm, out) for m in mods])
@@ -299,8 +303,9 @@ def main() -> int:
     dom = per_shape["gate_up_proj_M1"]
     roofline = {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                "kernel": "skinny4_kernel (decode product incl. DoRA x.A^T blocks and in-kernel epilogue), "
-                          "gate_up_proj 37888x3584 M=1",
+                "kernel": ("stream4_kernel (prepared tile-contiguous layout" if prep else
+                           "skinny4_kernel (row-aligned layout") +
+                          "; decode product incl. DoRA x.A^T blocks and in-kernel epilogue), gate_up_proj 37888x3584 M=1",
                 "bytes_per_launch": merged["gate_up_proj"].headline_bytes(), "avg_us": dom["us"]}
 
     # ---- prefill GEMM, M = 128 (config 2, the ridge: both fractions) and M = 2048

@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define WLQ_ABI_VERSION 3
+#define WLQ_ABI_VERSION 4
 
 enum wlq_status {
   WLQ_OK = 0,
@@ -103,6 +103,36 @@ int wlq_gemm(const void* X, const int32_t* q_packed, const void* lut_c, void* ou
              const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals,
              const float* lora_H, const void* lora_B, const void* dora_gamma, const void* lora_A,
              float lora_scale, int32_t r, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Bytes of the prepared (tile-contiguous) layout of a layer, or 0 when the
+ * layer has none (it needs 4-bit codes, a per-row LUT or a group size that is a
+ * multiple of 32, K % 8 == 0 and K < 65536).  nnz = number of outlier entries.
+ * No reference counterpart: the reference streams its row-aligned layout
+ * directly (csrc/gemv_kernel.cu:168-190); this layout is built once at load
+ * time, like the reference's own row-aligned repack (csrc/vllm_binding.cpp:198-236),
+ * so that the decode kernel reads whole 1 KB wave tiles. */
+size_t wlq_prepared_bytes(int64_t N, int64_t K, int32_t bits, int32_t group_size, int64_t nnz);
+
+/* Device: build the prepared layout from the reference-format tensors into
+ * `prepared` (256-byte aligned, wlq_prepared_bytes() bytes): codes in 16-row x
+ * 128-column tiles in MFMA lane order, LUT byte planes per 16-row tile, and per
+ * outlier its column and the fp32 delta fp16(e5m2 << 8) - lut[code] of the
+ * reference's GEMV outlier correction (csrc/gemv_kernel.cu:262-288). */
+int wlq_prepare(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K, int32_t bits, int32_t group_size,
+                const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz,
+                void* prepared, size_t prepared_bytes, hipStream_t stream);
+
+/* wlq_gemm with the layer's prepared layout: M <= 8 runs the streaming decode
+ * kernel on `prepared` (plus the reference chunk offsets), every other case the
+ * same kernels as wlq_gemm on the reference-format tensors, which stay required.
+ * Replaces the same reference launchers as wlq_gemm / wlq_gemv
+ * (csrc/vllm_binding.cpp:10-52, :318-419). */
+int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c, const void* prepared,
+                      size_t prepared_bytes, void* out, int64_t M, int64_t N, int64_t K, int32_t bits,
+                      int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets,
+                      const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz, const float* lora_H,
+                      const void* lora_B, const void* dora_gamma, const void* lora_A, float lora_scale, int32_t r,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Bit-exact W_out[N, K] (fp16) = lut[n, g(k), code(n, k)], outliers overwritten with e5m2 << 8.
  * Replaces launch_dequant_patch_metalog (csrc/gemm_kernel.cu:475-503, declared

@@ -21,6 +21,7 @@ Pins per function (all in tests/test_oracle_formats.py unless noted):
   fp16_bits_to_e5m2 / e5m2_to_fp16_bits    exhaustive vs torch.float8_e5m2 (off-tie values), hand ties
   build_chunk_csr                          dense-mask brute force, invariants, hand example
   dequant                                  closed form by loops, torch.gather special case, hand example
+  outlier_delta                            per-entry loops, lut + delta == w_true where exact, hand example
   ef_encode / ef_decode_*                  hand-built bitstream, round trip on random masks
   dora_gamma / merge_dora / lora_scale     closed form on hand matrices (tests/test_oracle_layer.py)
   linear_forward / lora_h                  brute-force loops, one-hot rows, r=0, linearity
@@ -271,6 +272,33 @@ def dequant(q, lut, N: int, K: int, bits: int, offsets=None, cols=None, vals=Non
         ok = gcols < K
         W[rows[ok], gcols[ok]] = e5m2_to_fp16_bits(np.asarray(vals)[ent[ok]])
     return W.astype(np.uint16).view(np.float16)
+
+
+def outlier_delta(q, lut, N: int, K: int, bits: int, offsets, cols, vals, group_size: int = 0):
+    """Per CSR entry (storage order): its global column and the fp32 correction
+    delta_w = fp32(fp16 bits (u8 << 8)) - fp32(lut[n, g(col), code(n, col)]) of the
+    reference GEMV's outlier pass (csrc/gemv_kernel.cu:268-286); entries with
+    column >= K are dropped there (`col < M`), here they get delta 0 and the
+    chunk's first column.  Returns (gcol int64 [nnz], delta float32 [nnz])."""
+    cols = np.asarray(cols)
+    nnz = cols.size
+    gcol = np.zeros(nnz, dtype=np.int64)
+    delta = np.zeros(nnz, dtype=np.float32)
+    if nnz == 0:
+        return gcol, delta
+    C = chunk_width(bits)
+    ent, rows, gc = csr_to_coo(offsets, cols, C)
+    codes = unpack_row_aligned(q, N, K, bits).astype(np.int64)
+    ng = num_groups(K, group_size)
+    lut16 = np.asarray(lut).view(np.uint16).reshape(N, ng, -1).view(np.float16)
+    ok = gc < K
+    gcol[ent] = np.where(ok, gc, (gc // C) * C)
+    okc = np.where(ok, gc, 0)
+    g = np.zeros_like(okc) if group_size <= 0 else np.minimum(okc // group_size, ng - 1)
+    w_true = e5m2_to_fp16_bits(np.asarray(vals)[ent]).view(np.float16).astype(np.float32)
+    w_lut = lut16[rows, g, codes[rows, okc]].astype(np.float32)
+    delta[ent] = np.where(ok, w_true - w_lut, np.float32(0.0)).astype(np.float32)
+    return gcol, delta
 
 
 # ---------------------------------------------------------------------------

@@ -51,6 +51,10 @@ def _declare(lib: ctypes.CDLL) -> None:
                                     c_i32, vp, c_sz, vp]),
         "wlq_gemm": (ctypes.c_int, [vp, vp, vp, vp, c_i64, c_i64, c_i64, c_i32, c_i64, c_i32, vp, vp, vp, vp, vp, vp,
                                     vp, c_f, c_i32, vp, c_sz, vp]),
+        "wlq_prepared_bytes": (c_sz, [c_i64, c_i64, c_i32, c_i32, c_i64]),
+        "wlq_prepare": (ctypes.c_int, [vp, vp, c_i64, c_i64, c_i32, c_i32, vp, vp, vp, c_i64, vp, c_sz, vp]),
+        "wlq_gemm_prepared": (ctypes.c_int, [vp, vp, vp, vp, c_sz, vp, c_i64, c_i64, c_i64, c_i32, c_i64, c_i32, vp,
+                                             vp, vp, c_i64, vp, vp, vp, vp, c_f, c_i32, vp, c_sz, vp]),
         "wlq_dequant": (ctypes.c_int, [vp, vp, vp, c_i64, c_i64, c_i32, c_i64, c_i32, vp, vp, vp, vp]),
         "wlq_dora_epilogue": (ctypes.c_int, [vp, vp, vp, vp, c_f, c_i32, c_i64, c_i64, vp]),
         "wlq_repack_row_aligned": (ctypes.c_int, [vp, c_i64, c_i64, c_i64, c_i32, vp, c_i64]),

@@ -4,9 +4,11 @@
 // binding (csrc/vllm_binding.cpp:455-532): gemv_forward, gemm_forward,
 // dequant_w0, init_workspaces, decode_ef_to_chunk_csr,
 // repack_q_indices_row_aligned.  Extensions are trailing defaulted arguments
-// only: group_size (LUT per group of columns) and lora_A (compute the DoRA H
-// inside the product instead of taking lora_h / lora_H).  Every device call goes through the C ABI of
-// libwlq_hip.so (include/wlq_abi.h) on torch's current HIP stream.
+// only: group_size (LUT per group of columns), lora_A (compute the DoRA H
+// inside the product instead of taking lora_h / lora_H) and prepared (the
+// layer's prepared layout from prepare_layer, an extra function).  Every
+// device call goes through the C ABI of libwlq_hip.so (include/wlq_abi.h) on
+// torch's current HIP stream.
 //
 // Differences from the reference, all stricter: dtypes, devices, contiguity and
 // sizes are checked before launch, unsupported bit widths raise instead of
@@ -87,6 +89,18 @@ torch::Tensor workspace_for(const torch::Device& dev, size_t bytes) {
 
 hipStream_t current_stream(const torch::Device& dev) { return c10::hip::getCurrentHIPStream(dev.index()).stream(); }
 
+// The prepared layout is a uint8 buffer built by prepare_layer (empty or absent: not used).
+const void* prepared_ptr(const c10::optional<torch::Tensor>& t, const torch::Device& dev) {
+  if (!t.has_value() || !t->defined() || t->numel() == 0) return nullptr;
+  check_dev(*t, "prepared", dev, torch::kUInt8);
+  return t->data_ptr();
+}
+
+int64_t nnz_of(const c10::optional<torch::Tensor>& cols, const int32_t* offs) {
+  if (offs == nullptr || !cols.has_value() || !cols->defined()) return 0;
+  return cols->numel();
+}
+
 }  // namespace
 
 void init_workspaces(int64_t max_N, int64_t max_K, torch::Device device) {
@@ -108,7 +122,7 @@ void gemv_forward(torch::Tensor q_packed, torch::Tensor lut_c, torch::Tensor x, 
                   c10::optional<torch::Tensor> chunk_cols, c10::optional<torch::Tensor> chunk_vals,
                   c10::optional<torch::Tensor> lora_B, c10::optional<torch::Tensor> lora_h,
                   c10::optional<torch::Tensor> dora_gamma, double lora_scale, int64_t group_size,
-                  c10::optional<torch::Tensor> lora_A) {
+                  c10::optional<torch::Tensor> lora_A, c10::optional<torch::Tensor> prepared) {
   const torch::Device dev = x.device();
   check_dev(q_packed, "q_packed", dev, torch::kInt32);
   check_dev(lut_c, "lut_c", dev, torch::kFloat16);
@@ -136,6 +150,15 @@ void gemv_forward(torch::Tensor q_packed, torch::Tensor lut_c, torch::Tensor x, 
   }
   const size_t need = wlq_gemm_workspace_bytes(1, N, K, (int32_t)bits, (h || !A) ? 0 : r, dev.index());
   torch::Tensor ws = workspace_for(dev, need);
+  const void* prep = prepared_ptr(prepared, dev);
+  if (prep != nullptr) {
+    check_status(wlq_gemm_prepared(x.data_ptr(), q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), prep,
+                                   (size_t)prepared->numel(), out.data_ptr(), 1, N, K, (int32_t)bits,
+                                   wlq_words_per_row(K, (int32_t)bits), (int32_t)group_size, offs, cols, vals,
+                                   nnz_of(chunk_cols, offs), h, B, g, A, (float)lora_scale, r, ws.data_ptr(),
+                                   (size_t)ws.numel(), current_stream(dev)));
+    return;
+  }
   check_status(wlq_gemv(q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), x.data_ptr(), out.data_ptr(), offs, cols,
                         vals, B, h, g, A, (float)lora_scale, r, N, K, (int32_t)bits, (int32_t)group_size,
                         ws.data_ptr(), (size_t)ws.numel(), current_stream(dev)));
@@ -146,7 +169,7 @@ void gemm_forward(torch::Tensor X, torch::Tensor q_packed, torch::Tensor lut_c, 
                   c10::optional<torch::Tensor> chunk_cols, c10::optional<torch::Tensor> chunk_vals,
                   c10::optional<torch::Tensor> lora_H, c10::optional<torch::Tensor> lora_B,
                   c10::optional<torch::Tensor> dora_gamma, double lora_scale, int64_t group_size,
-                  c10::optional<torch::Tensor> lora_A) {
+                  c10::optional<torch::Tensor> lora_A, c10::optional<torch::Tensor> prepared) {
   const torch::Device dev = X.device();
   check_dev(X, "X", dev, torch::kFloat16);
   check_dev(q_packed, "q_packed", dev, torch::kInt32);
@@ -175,6 +198,14 @@ void gemm_forward(torch::Tensor X, torch::Tensor q_packed, torch::Tensor lut_c, 
   }
   const size_t need = wlq_gemm_workspace_bytes(M, N, K, (int32_t)bits, (H || !A) ? 0 : r, dev.index());
   torch::Tensor ws = workspace_for(dev, need);
+  const void* prep = prepared_ptr(prepared, dev);
+  if (prep != nullptr) {
+    check_status(wlq_gemm_prepared(X.data_ptr(), q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), prep,
+                                   (size_t)prepared->numel(), out.data_ptr(), M, N, K, (int32_t)bits, words_per_row,
+                                   (int32_t)group_size, offs, cols, vals, nnz_of(chunk_cols, offs), H, B, g, A,
+                                   (float)lora_scale, r, ws.data_ptr(), (size_t)ws.numel(), current_stream(dev)));
+    return;
+  }
   check_status(wlq_gemm(X.data_ptr(), q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), out.data_ptr(), M, N, K,
                         (int32_t)bits, words_per_row, (int32_t)group_size, offs, cols, vals, H, B, g, A,
                         (float)lora_scale, r, ws.data_ptr(), (size_t)ws.numel(), current_stream(dev)));
@@ -200,6 +231,33 @@ void dequant_w0(torch::Tensor q_packed, torch::Tensor lut_c, torch::Tensor W_out
                            csr ? reinterpret_cast<const uint16_t*>(chunk_cols.data_ptr()) : nullptr,
                            csr ? reinterpret_cast<const uint8_t*>(chunk_vals.data_ptr()) : nullptr,
                            current_stream(dev)));
+}
+
+// Prepared (tile-contiguous) layout for the decode kernel, built on the device; an
+// empty tensor when the layer has none (wlq_prepared_bytes == 0).
+torch::Tensor prepare_layer(torch::Tensor q_packed, torch::Tensor lut_c, int64_t N, int64_t K, int64_t bits,
+                            int64_t group_size, c10::optional<torch::Tensor> chunk_offsets,
+                            c10::optional<torch::Tensor> chunk_cols, c10::optional<torch::Tensor> chunk_vals) {
+  const torch::Device dev = q_packed.device();
+  check_dev(q_packed, "q_packed", dev, torch::kInt32);
+  check_dev(lut_c, "lut_c", dev, torch::kFloat16);
+  TORCH_CHECK(bits >= 1 && bits <= 4, "prepare_layer: unsupported bits=", bits);
+  TORCH_CHECK(q_packed.numel() >= N * wlq_words_per_row(K, (int32_t)bits), "q_packed is too small");
+  check_lut(lut_c, N, K, bits, group_size);
+  check_csr(chunk_offsets, chunk_cols, chunk_vals, N, K, bits);
+  const int32_t* offs = opt_ptr<int32_t>(chunk_offsets, torch::kInt32, "chunk_offsets", dev);
+  const uint16_t* cols = cols_ptr(chunk_cols, dev);
+  const uint8_t* vals = opt_ptr<uint8_t>(chunk_vals, torch::kUInt8, "chunk_vals", dev);
+  const bool csr = offs && cols && vals;
+  const int64_t nnz = csr ? chunk_cols->numel() : 0;
+  const size_t bytes = wlq_prepared_bytes(N, K, (int32_t)bits, (int32_t)group_size, nnz);
+  auto opts = torch::TensorOptions().dtype(torch::kUInt8).device(dev);
+  if (bytes == 0) return torch::empty({0}, opts);
+  torch::Tensor buf = torch::empty({(int64_t)bytes}, opts);  // the caching allocator returns 512-byte aligned blocks
+  check_status(wlq_prepare(q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), N, K, (int32_t)bits, (int32_t)group_size,
+                           csr ? offs : nullptr, csr ? cols : nullptr, csr ? vals : nullptr, nnz, buf.data_ptr(),
+                           bytes, current_stream(dev)));
+  return buf;
 }
 
 std::tuple<torch::Tensor, torch::Tensor> decode_ef_to_chunk_csr(torch::Tensor ef_tile_meta, torch::Tensor ef_bitstream,
@@ -252,10 +310,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("lut_c"), py::arg("x"), py::arg("out"), py::arg("N"), py::arg("K"), py::arg("bits"),
         py::arg("chunk_offsets") = py::none(), py::arg("chunk_cols") = py::none(), py::arg("chunk_vals") = py::none(),
         py::arg("lora_B") = py::none(), py::arg("lora_h") = py::none(), py::arg("dora_gamma") = py::none(),
-        py::arg("lora_scale") = 1.0, py::arg("group_size") = 0, py::arg("lora_A") = py::none());
+        py::arg("lora_scale") = 1.0, py::arg("group_size") = 0, py::arg("lora_A") = py::none(),
+        py::arg("prepared") = py::none());
   m.def("gemm_forward", &gemm_forward, "WLQ product for M activation rows", py::arg("X"), py::arg("q_packed"),
         py::arg("lut_c"), py::arg("out"), py::arg("N"), py::arg("K"), py::arg("bits"), py::arg("words_per_row"),
         py::arg("chunk_offsets") = py::none(), py::arg("chunk_cols") = py::none(), py::arg("chunk_vals") = py::none(),
         py::arg("lora_H") = py::none(), py::arg("lora_B") = py::none(), py::arg("dora_gamma") = py::none(),
-        py::arg("lora_scale") = 1.0, py::arg("group_size") = 0, py::arg("lora_A") = py::none());
+        py::arg("lora_scale") = 1.0, py::arg("group_size") = 0, py::arg("lora_A") = py::none(),
+        py::arg("prepared") = py::none());
+  m.def("prepare_layer", &prepare_layer, "Prepared (tile-contiguous) layout of a layer for the decode kernel",
+        py::arg("q_packed"), py::arg("lut_c"), py::arg("N"), py::arg("K"), py::arg("bits"), py::arg("group_size") = 0,
+        py::arg("chunk_offsets") = py::none(), py::arg("chunk_cols") = py::none(), py::arg("chunk_vals") = py::none());
 }

@@ -6,6 +6,7 @@
 // invalid argument returns a status before anything is launched.  The CU count
 // used for split planning is cached per device (the reference caches the first
 // device's value for all devices, csrc/gemv_kernel.cu:355-363).
+#include <algorithm>
 #include <atomic>
 
 #include "wlq_abi.h"
@@ -207,8 +208,48 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
   const size_t hb = (r > 0 && !fused) ? round_up((size_t)M * r * sizeof(float)) : 0;
   const wlq::SplitPlan p = skinny ? wlq::plan_skinny(L, (int)M, cus, unlimited, fused ? r : 0)
                                   : wlq::plan_gemm(L, (int)M, cus, unlimited);
-  const size_t need = hb + p.workspace_bytes;
+  size_t need = hb + p.workspace_bytes;
+  if (M <= wlq::stream_max_m() && bits == 4) {  // the prepared-layout kernel may serve the call
+    const wlq::StreamPlan sp = wlq::plan_stream((int)N, (int)K, (int)M, cus, r > 0 && r <= wlq::stream_max_rank() ? r : 0);
+    need = std::max(need, sp.workspace_bytes + 256);
+  }
   return need > 0 ? wlq::kSyncBytes + need : 0;
+}
+
+size_t wlq_prepared_bytes(int64_t N, int64_t K, int32_t bits, int32_t group_size, int64_t nnz) {
+  if (N <= 0 || K <= 0 || N > 0x3fffffff || K > 0x3fffffff || nnz < 0 || group_size < 0) return 0;
+  const int gs = (group_size > 0 && group_size >= K) ? 0 : group_size;
+  if (!wlq::prepared_supported((int)N, (int)K, bits, gs)) return 0;
+  return wlq::prepared_layout((int)N, (int)K, gs, nnz).bytes;
+}
+
+int wlq_prepare(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K, int32_t bits, int32_t group_size,
+                const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz,
+                void* prepared, size_t prepared_bytes, hipStream_t stream) {
+  wlq::Layer L{};
+  int st = make_layer(q_packed, lut_c, N, K, bits, -1, group_size, chunk_offsets, chunk_cols, chunk_vals,
+                      "wlq_prepare", &L);
+  if (st != WLQ_OK) return st;
+  if (nnz < 0 || (L.offsets == nullptr && nnz != 0)) {
+    wlq::set_error("wlq_prepare: nnz=%lld does not match the outlier arrays", (long long)nnz);
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  if (!wlq::prepared_supported(L.N, L.K, L.bits, L.group_size)) {
+    wlq::set_error("wlq_prepare: no prepared layout for bits=%d, group_size=%d, K=%lld (needs 4-bit, a per-row LUT "
+                   "or a group size multiple of 32, K %% 8 == 0, K < 65536)",
+                   (int)bits, (int)group_size, (long long)K);
+    return WLQ_ERR_UNSUPPORTED;
+  }
+  const size_t need = wlq::prepared_layout(L.N, L.K, L.group_size, nnz).bytes;
+  if (prepared == nullptr || prepared_bytes < need) {
+    wlq::set_error("wlq_prepare: the prepared buffer needs %zu bytes (got %zu)", need, prepared_bytes);
+    return prepared == nullptr ? WLQ_ERR_NULL_POINTER : WLQ_ERR_CAPACITY;
+  }
+  if ((reinterpret_cast<uintptr_t>(prepared) & 255u) != 0) {
+    wlq::set_error("wlq_prepare: the prepared buffer must be 256-byte aligned");
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  return hip_status(wlq::launch_prepare(L, nnz, prepared, stream), "wlq_prepare");
 }
 
 int wlq_gemv(const int32_t* q_packed, const void* lut_c, const void* x, void* out, const int32_t* chunk_offsets,
@@ -234,6 +275,48 @@ int wlq_gemm(const void* X, const int32_t* q_packed, const void* lut_c, void* ou
   if (st != WLQ_OK) return st;
   const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_A, lora_scale, r);
   return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, "wlq_gemm");
+}
+
+int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c, const void* prepared,
+                      size_t prepared_bytes, void* out, int64_t M, int64_t N, int64_t K, int32_t bits,
+                      int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets,
+                      const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz, const float* lora_H,
+                      const void* lora_B, const void* dora_gamma, const void* lora_A, float lora_scale, int32_t r,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  wlq::Layer L{};
+  int st = make_layer(q_packed, lut_c, N, K, bits, words_per_row, group_size, chunk_offsets, chunk_cols, chunk_vals,
+                      "wlq_gemm_prepared", &L);
+  if (st != WLQ_OK) return st;
+  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_A, lora_scale, r);
+  if (prepared != nullptr && M >= 1 && M <= wlq::stream_max_m() && L.N > 0 && X != nullptr && out != nullptr &&
+      wlq::prepared_supported(L.N, L.K, L.bits, L.group_size) && nnz >= 0 && (L.offsets != nullptr || nnz == 0)) {
+    const size_t need = wlq::prepared_layout(L.N, L.K, L.group_size, nnz).bytes;
+    if (prepared_bytes < need) {
+      wlq::set_error("wlq_gemm_prepared: the prepared buffer holds %zu bytes, the layer needs %zu (nnz=%lld)",
+                     prepared_bytes, need, (long long)nnz);
+      return WLQ_ERR_CAPACITY;
+    }
+    const bool fused_h = D.r > 0 && D.H == nullptr;
+    // the kernel stages B rows with 16-byte loads (r % 8 == 0) and x / lora_A rows likewise
+    const bool dora_ok = D.r == 0 || (D.r % 8 == 0 && D.r <= wlq::stream_max_rank() &&
+                                      (reinterpret_cast<uintptr_t>(D.B) & 15u) == 0);
+    const bool aligned = (reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (reinterpret_cast<uintptr_t>(prepared) & 255u) == 0 &&
+                         (!fused_h || (reinterpret_cast<uintptr_t>(D.A) & 15u) == 0) && dora_ok;
+    const wlq::StreamPlan p =
+        wlq::plan_stream(L.N, L.K, (int)M, current_cu_count(), fused_h ? D.r : 0);
+    const bool need_sync = p.splits > 1 || fused_h;
+    const size_t ws = workspace != nullptr ? workspace_bytes : 0;
+    const bool ws_ok = !need_sync || ws >= wlq::kSyncBytes + p.workspace_bytes;
+    if (p.ok && aligned && ws_ok && (!fused_h || D.r <= wlq::stream_max_rank())) {
+      char* wbase = reinterpret_cast<char*>(workspace);
+      uint32_t* sync = need_sync ? reinterpret_cast<uint32_t*>(wbase) : nullptr;
+      float* w = need_sync ? reinterpret_cast<float*>(wbase + wlq::kSyncBytes) : nullptr;
+      return hip_status(wlq::launch_stream(L, prepared, nnz, D, reinterpret_cast<const uint16_t*>(X),
+                                           reinterpret_cast<uint16_t*>(out), (int)M, p, w, sync, stream),
+                        "wlq_gemm_prepared");
+    }
+  }
+  return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, "wlq_gemm_prepared");
 }
 
 int wlq_dequant(const int32_t* q_packed, const void* lut_c, void* W_out, int64_t N, int64_t K, int32_t bits,

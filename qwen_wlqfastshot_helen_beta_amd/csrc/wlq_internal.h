@@ -61,6 +61,30 @@ hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_
 
 hipError_t launch_dequant(const Layer& L, uint16_t* W, hipStream_t stream);
 
+// Prepared (tile-contiguous) layout of a 4-bit layer for the streaming decode kernel
+// (wlq_stream.hip): byte offsets of its four parts inside one buffer.
+struct PreparedLayout {
+  int T, S, ng;             // row tiles of 16, slabs of 128 columns, LUT groups per row
+  size_t codes_off, planes_off, gcol_off, delta_off, bytes;
+};
+bool prepared_supported(int N, int K, int bits, int group_size);
+PreparedLayout prepared_layout(int N, int K, int group_size, int64_t nnz);
+hipError_t launch_prepare(const Layer& L, int64_t nnz, void* prepared, hipStream_t stream);
+
+struct StreamPlan {
+  int tpb;                  // row tiles per block (1 or 4)
+  int TB, splits, cps;      // tile blocks, K splits, outlier chunks per split
+  int h_blocks;             // DoRA blocks when H is computed in the kernel
+  size_t hfin_off, hpart_off, partial_off, workspace_bytes;
+  bool ok;
+};
+int stream_max_m();
+int stream_max_rank();
+StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank);
+hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, const Dora& D, const uint16_t* x,
+                         uint16_t* out, int M, const StreamPlan& plan, float* workspace, uint32_t* sync,
+                         hipStream_t stream);
+
 // out = fp16_rn(sum of fp32 split-K partials [splits, M, N]) (epilogue already applied).
 hipError_t launch_splitk_sum(const float* partial, int splits, int M, int N, uint16_t* out, hipStream_t stream);
 

@@ -1,0 +1,759 @@
+// Decode product on the prepared (tile-contiguous) layout: M = 1..8 activation
+// rows, 4-bit codes, per-row LUTs or LUT groups of a multiple of 32 columns.
+//
+// Reference behaviour replaced: gemv_chunk_csr_kernel + launch_gemv_chunk_csr
+// (csrc/gemv_kernel.cu:86-320, :396-457) and the split-K reduce
+// (csrc/gemv_kernel.cu:322-353) for M == 1, gemm_metalog_dora_kernel
+// (csrc/gemm_kernel.cu:32-294) for 2 <= M < 16.  Same arithmetic: W0 rows
+// expanded through their LUTs, the delta-form outlier correction
+// (w_true - lut[code]) * x (csrc/gemv_kernel.cu:262-288), the DoRA epilogue
+// fp16_rn((acc + s * h.B) * gamma) (csrc/gemv_kernel.cu:305-319).
+//
+// Prepared layout (built once per layer by the prepare kernels below, from the
+// reference's row-aligned codes, LUTs and chunk CSR):
+//   codes  u32x4 [T][S][64]     T = ceil(N/16) row tiles, S = ceil(K/128) slabs;
+//                               lane l = r + 16*kq holds the 32 codes of row
+//                               16t + r, columns 128s + 32kq .. +31 (4 words), so
+//                               one wave load is 1 KB contiguous and lands in the
+//                               MFMA B-operand lane order.
+//   planes u32x4 [T][ng][2][16] the low and the high bytes of the 16 fp16 LUT
+//                               entries of row 16t + r, group g (the V_PERM_B32
+//                               byte planes, wlq_device.h).
+//   gcol   u16 [nnz]            the outlier's column (chunk base + chunk column).
+//   delta  f32 [nnz]            fp32(fp16(e5m2 << 8)) - fp32(lut[code]): the
+//                               reference's delta_w, computed once.
+// The reference's chunk offsets are used as they are.
+//
+// Work decomposition.  The grid is the DoRA blocks (x.A^T partial sums over 512
+// columns, when H is computed here) followed by tile blocks x K splits.  A tile
+// block is 4 waves on TPB row tiles (16 rows each); the WPT = 4 / TPB waves of a
+// tile take its slabs round-robin.  Blocks are small (tens of KB of weights) and
+// many (~4 per CU or more), so the hardware dispatcher balances them.  Per slab a
+// lane dequantizes its 4 code words through its row's byte planes and feeds four
+// V_MFMA_F32_16X16X32_F16 (A = activation rows from LDS, B = W rows); slabs are
+// prefetched kPF ahead into registers.  After the slabs, the block's threads walk
+// its rows' outlier entries (col, delta) and the wave partials are summed in a
+// fixed order.  One K split: the block applies the epilogue.  Several: fp32
+// partials go to the workspace and the block that counts the last arrival on its
+// tile block sums them in split order and applies the epilogue.
+//
+// DoRA H: the DoRA blocks have the lowest block indices, so they are dispatched
+// before every tile block.  The last of them rounds H to fp16 and raises a ready
+// flag; a block that needs H waits for the flag (normally long set by then).  The
+// last block to finish resets the flag and the counters, so every call leaves
+// them zero.
+#include <algorithm>
+
+#include "wlq_device.h"
+#include "wlq_internal.h"
+
+namespace wlq {
+namespace {
+
+#ifndef WLQ_STREAM_PF
+#define WLQ_STREAM_PF 4
+#endif
+#ifndef WLQ_STREAM_BLOCKS_PER_CU
+#define WLQ_STREAM_BLOCKS_PER_CU 4
+#endif
+#ifndef WLQ_STREAM_WAVES_PER_EU
+#define WLQ_STREAM_WAVES_PER_EU 5
+#endif
+constexpr int kPF = WLQ_STREAM_PF;  // slabs in flight per wave
+constexpr int kEB = 2;          // outlier entries per thread fetched during the slab loop
+constexpr int kXR = 4;          // 16-byte activation units per thread (the planner bounds the staging)
+constexpr int kHCols = 512;     // columns per DoRA block
+constexpr int kMaxRank = 64;
+constexpr int kXBudget = 16384; // activation staging bytes per block
+constexpr int kBlocksPerCU = WLQ_STREAM_BLOCKS_PER_CU;  // tile-block target per CU
+constexpr uint32_t kSpinLimit = 1u << 24;
+
+// Sync words in the workspace's counter area (all zero between calls).
+constexpr int kSyncDora = 0;      // DoRA blocks arrived (reset by the last of them)
+constexpr int kSyncSlot0 = 64;    // ready slots: word 0 = H published, word 1 = consumers counted
+constexpr int kSlotWords = 16;    // one 64-byte line per slot
+constexpr int kMaxSlots = 128;    // tile block tb uses slot tb % min(TB, kMaxSlots)
+constexpr int kSyncTile = kSyncSlot0 + kSlotWords * kMaxSlots;  // [TB] split arrivals per tile block
+
+struct StreamArgs {
+  const u32x4_t* codes;
+  const u32x4_t* planes;
+  const uint16_t* gcol;
+  const float* delta;
+  const int32_t* offsets;  // [N, nch + 1] (null: no outliers)
+  const uint16_t* x;
+  uint16_t* out;
+  const uint16_t* B;
+  const float* H;          // caller's H, or null (DoRA blocks compute it when A is set)
+  const uint16_t* gamma;
+  const uint16_t* A;
+  float scale;
+  int r;
+  int M, N, K, S, ng, nch, T, TB;
+  uint32_t g_magic;        // floor(c / G) == umulhi(c, g_magic) for c < 2^20
+  int splits, cps;         // K splits per tile block, outlier chunks per split
+  int xstride;             // halves per staged activation row
+  int h_blocks;
+  float* partial;          // [splits, M, N]
+  float* hpart;            // [h_blocks, M, r]
+  float* hfin;             // [M, r]
+  uint32_t* sync;
+};
+
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_dev(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Stores are device-scope (coherent across the XCDs' L2s); waiting for them to
+// complete orders them before a following arrival count.
+__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+__device__ __forceinline__ int group_of(int col, uint32_t magic) { return (int)__umulhi((uint32_t)col, magic); }
+
+// ------------------------------------------------------------------ DoRA blocks
+
+// hpart[hb, i, j] = sum over columns [512 hb, +512) of x[i, k] * A[j, k]; wave w
+// covers 128 columns with MFMA 16x16x32 (A = activation rows, B = lora_A rows,
+// both in natural column order); the four wave sums are added through LDS.  The
+// block that arrives last rounds H = fp16(sum over hb) and publishes it.
+__device__ void dora_block(const StreamArgs& a, int hb, float* red) {
+  constexpr int JT = kMaxRank / 16;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int jt_n = (a.r + 15) >> 4;
+  float4_t acc[JT];
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt) acc[jt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const int kbase = hb * kHCols + wave * 128;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int k = kbase + 32 * ks + 8 * kq;
+    const bool kin = k < a.K;  // K % 8 == 0: an 8-column unit is all inside or all outside
+    u32x4_t xa = {0u, 0u, 0u, 0u};
+    if (r16 < a.M && kin) xa = *reinterpret_cast<const u32x4_t*>(a.x + (size_t)r16 * a.K + k);
+    u32x4_t ab[JT];
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) {
+      const int j = 16 * jt + r16;
+      ab[jt] = u32x4_t{0u, 0u, 0u, 0u};
+      if (jt < jt_n && j < a.r && kin) ab[jt] = *reinterpret_cast<const u32x4_t*>(a.A + (size_t)j * a.K + k);
+    }
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt)
+      if (jt < jt_n) acc[jt] = mfma16x16x32(xa, ab[jt], acc[jt]);
+  }
+  // red[wave][jt][e][lane]
+#pragma unroll
+  for (int jt = 0; jt < JT; ++jt)
+    if (jt < jt_n)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[((wave * JT + jt) * 4 + e) * 64 + lane] = acc[jt][e];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < jt_n * 256; idx += blockDim.x) {
+    const int ln = idx & 63;
+    const int e = (idx >> 6) & 3;
+    const int jt = idx >> 8;
+    const int i = 4 * (ln >> 4) + e;
+    const int j = 16 * jt + (ln & 15);
+    if (i < a.M && j < a.r) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) v += red[((w * JT + jt) * 4 + e) * 64 + ln];
+      store_dev(a.hpart + ((size_t)hb * a.M + i) * a.r + j, v);
+    }
+  }
+  stores_done();
+  __syncthreads();
+  __shared__ int s_last;
+  if (threadIdx.x == 0) s_last = atomicAdd(a.sync + kSyncDora, 1u) == (uint32_t)(a.h_blocks - 1);
+  __syncthreads();
+  if (!s_last) return;
+  compiler_fence();
+  for (int idx = threadIdx.x; idx < a.M * a.r; idx += blockDim.x) {
+    float v = 0.f;
+    for (int b = 0; b < a.h_blocks; ++b) v += load_dev(a.hpart + (size_t)b * a.M * a.r + idx);
+    store_dev(a.hfin + idx, h2f(f2h_rn(v)));  // the reference's F.linear output is fp16
+  }
+  stores_done();
+  __syncthreads();
+  // H is visible: raise every ready slot, then reset the arrival count for the next call
+  const int slots = min(a.TB, kMaxSlots);
+  for (int g = threadIdx.x; g < slots; g += blockDim.x) store_dev(a.sync + kSyncSlot0 + kSlotWords * g, 1u);
+  if (threadIdx.x == 0) store_dev(a.sync + kSyncDora, 0u);
+}
+
+// --------------------------------------------------------------- tile blocks
+
+struct Slab {
+  u32x4_t codes;
+  u32x4_t lo, hi;
+};
+
+// Waits until the block's ready slot is raised (bounded: a wait that never ends is
+// cut off after kSpinLimit polls rather than hang the GPU).
+__device__ __forceinline__ void wait_h_ready(const uint32_t* slot) {
+  if (threadIdx.x == 0) {
+    uint32_t spins = 0;
+    while (load_dev(slot) == 0u && ++spins < kSpinLimit) __builtin_amdgcn_s_sleep(2);
+  }
+  __syncthreads();
+  compiler_fence();
+}
+
+template <bool PER_ROW, int TPB, int MB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WLQ_STREAM_WAVES_PER_EU)))
+void stream4_kernel(const StreamArgs a) {
+  constexpr int WPT = 4 / TPB;       // waves per row tile
+  constexpr int ROWS = 16 * TPB;     // output rows per block
+  constexpr int TPR = 256 / ROWS;    // threads per row in the outlier pass
+  extern __shared__ __align__(16) uint16_t smem[];
+
+  int bid = blockIdx.x;
+  if (bid < a.h_blocks) {
+    dora_block(a, bid, reinterpret_cast<float*>(smem));
+    return;
+  }
+  bid -= a.h_blocks;
+  const int tb = bid / a.splits;
+  const int split = bid - tb * a.splits;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: slab indices live in SGPRs
+  const int r = lane & 15;
+  const int kq = lane >> 4;
+  const int t = min(tb * TPB + wave / WPT, a.T - 1);
+  const int ph = wave % WPT;
+  const int c0 = split * a.cps;
+  const int c1 = min(a.nch, c0 + a.cps);
+  const int s0 = 4 * c0;
+  const int s1 = min(a.S, 4 * c1);
+  const int nw = (s1 - s0 - ph + WPT - 1) / WPT;  // this wave's slabs (may be 0)
+  const int s_last = min(s0 + ph + WPT * max(nw - 1, 0), s1 - 1);  // prefetch clamp (in range)
+
+  // LDS: [x: M rows x xstride halves][64 B zeros][red: 4 x 256 f32][corr: MB x ROWS f32][H: M x r f32]
+  //      [B rows: ROWS x r halves][gamma: ROWS halves]
+  uint16_t* xs = smem;
+  const int xbytes = ((a.M * a.xstride * 2) + 15) & ~15;
+  uint16_t* zline = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(smem) + xbytes);
+  float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(zline) + 64);
+  float* cres = red + 4 * 256;
+  float* hs = cres + MB * ROWS;
+  uint16_t* bs = reinterpret_cast<uint16_t*>(hs + a.M * max(a.r, 1));
+  uint16_t* gs = bs + ROWS * a.r;
+
+  // Outlier pass mapping: thread (rho, j) walks entries j, j + TPR, ... of block row rho.
+  const int rho = threadIdx.x / TPR;
+  const int jr = threadIdx.x - rho * TPR;
+  const int n_out = tb * ROWS + rho;
+  const bool csr = a.offsets != nullptr;
+  int e0 = 0, e1 = 0;
+  if (csr && n_out < a.N) {
+    const int32_t* offr = a.offsets + (size_t)n_out * (a.nch + 1);
+    e0 = offr[c0];
+    e1 = offr[c1];
+  }
+
+  // Activations [s0*128, s1*128) of the M rows: loads now, LDS stores after the prefetch is issued.
+  const int upr = (s1 - s0) * 16;  // 8-column units per row
+  const int total = a.M * upr;
+  u32x4_t xv[kXR];
+#pragma unroll
+  for (int k = 0; k < kXR; ++k) {
+    const int u = min((int)threadIdx.x + 256 * k, max(total - 1, 0));
+    const int i = u / upr;
+    const int col = min(s0 * 128 + ((u - i * upr) << 3), a.K - 8);
+    xv[k] = *reinterpret_cast<const u32x4_t*>(a.x + (size_t)i * a.K + col);
+  }
+
+  // DoRA B rows and gamma of the block's rows (16-byte units; r % 8 == 0, checked by the host).
+  const int bupr = a.r >> 3;
+  const int btotal = ROWS * bupr;
+  u32x4_t bv[2];
+  uint16_t gv = 0;
+  if (a.r > 0) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int u = min((int)threadIdx.x + 256 * k, btotal - 1);
+      const int row = min(tb * ROWS + u / bupr, a.N - 1);
+      bv[k] = *reinterpret_cast<const u32x4_t*>(a.B + (size_t)row * a.r + 8 * (u % bupr));
+    }
+    gv = a.gamma[min(tb * ROWS + (int)(threadIdx.x % ROWS), a.N - 1)];
+  }
+
+  // Slab prefetch.
+  const u32x4_t* qb = a.codes + (size_t)t * a.S * 64 + lane;
+  const u32x4_t* lb = a.planes + (size_t)t * a.ng * 32 + r;
+  auto load_slab = [&](Slab& sl, int s) __attribute__((always_inline)) {
+    sl.codes = qb[(size_t)s * 64];
+    if constexpr (!PER_ROW) {
+      const int g = min(group_of(128 * s + 32 * kq, a.g_magic), a.ng - 1);
+      sl.lo = lb[g * 32];
+      sl.hi = lb[g * 32 + 16];
+    }
+  };
+  LutPlanes<4> pl;
+  if constexpr (PER_ROW) {
+    const u32x4_t lo = lb[0];
+    const u32x4_t hi = lb[16];
+    pl.lo[0] = lo.x; pl.lo[1] = lo.y; pl.lo[2] = lo.z; pl.lo[3] = lo.w;
+    pl.hi[0] = hi.x; pl.hi[1] = hi.y; pl.hi[2] = hi.z; pl.hi[3] = hi.w;
+  }
+  Slab buf[kPF];
+#pragma unroll
+  for (int u = 0; u < kPF; ++u) load_slab(buf[u], min(s0 + ph + WPT * u, s_last));
+
+#pragma unroll
+  for (int k = 0; k < kXR; ++k) {
+    const int u = (int)threadIdx.x + 256 * k;
+    if (u < total) {
+      const int i = u / upr;
+      const int c8 = u - i * upr;
+      const bool inside = s0 * 128 + (c8 << 3) < a.K;  // K % 8 == 0
+      *reinterpret_cast<u32x4_t*>(xs + i * a.xstride + (c8 << 3)) =
+          inside ? permute_p(xv[k]) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zline)[threadIdx.x] = 0u;
+  if (a.r > 0) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int u = (int)threadIdx.x + 256 * k;
+      if (u < btotal) *reinterpret_cast<u32x4_t*>(bs + 8 * u) = bv[k];
+    }
+    if (threadIdx.x < ROWS) gs[threadIdx.x] = gv;
+  }
+
+  // Outlier entries, fetched while the slabs stream (clamped, so the loads are unconditional).
+  uint32_t ecol[kEB];
+  float edel[kEB];
+  if (csr) {
+#pragma unroll
+    for (int u = 0; u < kEB; ++u) {
+      const int e = min(e0 + jr + TPR * u, max(e1 - 1, 0));
+      ecol[u] = a.gcol[e];
+      edel[u] = a.delta[e];
+    }
+  }
+  __syncthreads();
+
+  // Slab loop.
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow = (r < a.M) ? xs + r * a.xstride + kq * 32 : nullptr;
+  auto consume = [&](const Slab& sl, int s) __attribute__((always_inline)) {
+    LutPlanes<4> t4;
+    if constexpr (PER_ROW) {
+      t4 = pl;
+    } else {
+      t4.lo[0] = sl.lo.x; t4.lo[1] = sl.lo.y; t4.lo[2] = sl.lo.z; t4.lo[3] = sl.lo.w;
+      t4.hi[0] = sl.hi.x; t4.hi[1] = sl.hi.y; t4.hi[2] = sl.hi.z; t4.hi[3] = sl.hi.w;
+    }
+    const uint16_t* xp = xrow ? xrow + (s - s0) * 128 : zline;
+    const uint32_t w[4] = {sl.codes.x, sl.codes.y, sl.codes.z, sl.codes.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      uint32_t b[4];
+      dequant_word4(w[q], t4, b);
+      const u32x4_t bv = {b[0], b[1], b[2], b[3]};
+      const u32x4_t av = *reinterpret_cast<const u32x4_t*>(xp + (xrow ? 8 * q : 0));
+      acc = mfma16x16x32(av, bv, acc);
+    }
+  };
+  // Steady state: every slot consumed is reloaded kPF slabs ahead; then one round with
+  // conditional reloads and a last round without (nw is wave-uniform).
+  int j0 = 0;
+  for (; j0 + 2 * kPF <= nw; j0 += kPF) {
+#pragma unroll
+    for (int u = 0; u < kPF; ++u) {
+      consume(buf[u], s0 + ph + WPT * (j0 + u));
+      load_slab(buf[u], s0 + ph + WPT * (j0 + u + kPF));
+      __builtin_amdgcn_sched_barrier(0);  // keep each reload right behind its slot's use
+    }
+  }
+  if (j0 < nw) {
+#pragma unroll
+    for (int u = 0; u < kPF; ++u) {
+      if (j0 + u < nw) {
+        consume(buf[u], s0 + ph + WPT * (j0 + u));
+        if (j0 + u + kPF < nw) load_slab(buf[u], s0 + ph + WPT * (j0 + u + kPF));
+      }
+    }
+    j0 += kPF;
+#pragma unroll
+    for (int u = 0; u < kPF; ++u)
+      if (j0 + u < nw) consume(buf[u], s0 + ph + WPT * (j0 + u));
+  }
+
+  // Wave partials: red[wave][e][lane] = D[i = 4 kq + e][row r].
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[(wave * 4 + e) * 64 + lane] = acc[e];
+
+  // Outliers: corr[i] = sum over the thread's entries of delta * x[i, col].
+  float corr[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) corr[i] = 0.f;
+  if (csr) {
+    const int xc0 = s0 * 128;
+    auto entry = [&](uint32_t col, float d) __attribute__((always_inline)) {
+      const int xc = (int)col - xc0;
+      const int xi = (xc & ~7) + p_slot(xc & 7);
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        if (i < a.M) corr[i] += d * h2f(xs[i * a.xstride + xi]);
+    };
+#pragma unroll
+    for (int u = 0; u < kEB; ++u)
+      if (e0 + jr + TPR * u < e1) entry(ecol[u], edel[u]);
+    for (int e = e0 + jr + TPR * kEB; e < e1; e += TPR) entry(a.gcol[e], a.delta[e]);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      if (i < a.M) {
+        float v = corr[i];
+#pragma unroll
+        for (int m = TPR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+        corr[i] = v;
+      }
+    }
+    if (jr == 0) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        if (i < a.M) cres[i * ROWS + rho] = corr[i];
+    }
+  }
+  __syncthreads();
+
+  // Block sums for the outputs (i, rho): wave partials in phase order, then the outliers.
+  const int nouts = a.M * ROWS;
+  constexpr int kOPT = (MB * ROWS + 255) / 256;  // outputs per thread
+  float v[kOPT];
+#pragma unroll
+  for (int q = 0; q < kOPT; ++q) {
+    const int o = (int)threadIdx.x + 256 * q;
+    v[q] = 0.f;
+    if (o < nouts) {
+      const int i = o / ROWS;
+      const int rr = o - i * ROWS;
+      const int tl = rr >> 4;
+      const int ln = (rr & 15) + 16 * (i >> 2);
+      float s = 0.f;
+#pragma unroll
+      for (int p = 0; p < WPT; ++p) s += red[((tl * WPT + p) * 4 + (i & 3)) * 64 + ln];
+      if (csr) s += cres[i * ROWS + rr];
+      v[q] = s;
+    }
+  }
+
+  if (a.splits > 1) {
+#pragma unroll
+    for (int q = 0; q < kOPT; ++q) {
+      const int o = (int)threadIdx.x + 256 * q;
+      if (o < nouts) {
+        const int i = o / ROWS;
+        const int n = tb * ROWS + (o - i * ROWS);
+        if (n < a.N) store_dev(a.partial + ((size_t)split * a.M + i) * a.N + n, v[q]);
+      }
+    }
+    stores_done();
+    __syncthreads();
+    __shared__ int s_last;
+    if (threadIdx.x == 0) s_last = atomicAdd(a.sync + kSyncTile + tb, 1u) == (uint32_t)(a.splits - 1);
+    __syncthreads();
+    if (!s_last) return;
+    compiler_fence();
+#pragma unroll
+    for (int q = 0; q < kOPT; ++q) {
+      const int o = (int)threadIdx.x + 256 * q;
+      if (o < nouts) {
+        const int i = o / ROWS;
+        const int n = tb * ROWS + (o - i * ROWS);
+        if (n < a.N) {
+          float s = 0.f;
+          for (int sp = 0; sp < a.splits; ++sp) s += load_dev(a.partial + ((size_t)sp * a.M + i) * a.N + n);
+          v[q] = s;
+        }
+      }
+    }
+    if (threadIdx.x == 0) store_dev(a.sync + kSyncTile + tb, 0u);
+  }
+
+  // Epilogue: y = fp16_rn((v + s * H[i, :] . B[n, :]) * gamma[n]) with H, B and gamma from LDS.
+  const int slots = min(a.TB, kMaxSlots);
+  uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
+  if (a.r > 0) {
+    if (a.h_blocks > 0) {
+      wait_h_ready(slot);
+      for (int idx = threadIdx.x; idx < a.M * a.r; idx += 256) hs[idx] = load_dev(a.hfin + idx);
+    } else {
+      for (int idx = threadIdx.x; idx < a.M * a.r; idx += 256) hs[idx] = a.H[idx];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < kOPT; ++q) {
+    const int o = (int)threadIdx.x + 256 * q;
+    if (o < nouts) {
+      const int i = o / ROWS;
+      const int rr = o - i * ROWS;
+      const int n = tb * ROWS + rr;
+      if (n < a.N) {
+        float y = v[q];
+        if (a.r > 0) {
+          float ls = 0.f;
+          const float* hi = hs + i * a.r;
+          const uint16_t* bb = bs + rr * a.r;
+          for (int j = 0; j < a.r; j += 8) {
+            const u32x4_t b8 = *reinterpret_cast<const u32x4_t*>(bb + j);
+            const uint32_t w4[4] = {b8.x, b8.y, b8.z, b8.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              ls += hi[j + 2 * e] * h2f((uint16_t)(w4[e] & 0xFFFFu));
+              ls += hi[j + 2 * e + 1] * h2f((uint16_t)(w4[e] >> 16));
+            }
+          }
+          y = (y + a.scale * ls) * h2f(gs[rr]);
+        }
+        a.out[(size_t)i * a.N + n] = f2h_rn(y);
+      }
+    }
+  }
+  if (a.r > 0 && a.h_blocks > 0 && threadIdx.x == 0) {
+    // count this consumer; the slot's last consumer lowers it for the next call
+    const int g = tb % slots;
+    const uint32_t members = (uint32_t)(a.TB / slots + (g < a.TB % slots ? 1 : 0));
+    if (atomicAdd(slot + 1, 1u) == members - 1u) {
+      store_dev(slot + 1, 0u);
+      store_dev(slot, 0u);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- preparation
+
+__global__ __launch_bounds__(256) void prep_codes_kernel(const uint32_t* __restrict__ q, int N, int wpr, int T, int S,
+                                                         u32x4_t* __restrict__ codes) {
+  const size_t total = (size_t)T * S * 64;
+  for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
+    const int l = (int)(idx & 63);
+    const size_t ts = idx >> 6;
+    const int s = (int)(ts % (size_t)S);
+    const int t = (int)(ts / (size_t)S);
+    const int n = 16 * t + (l & 15);
+    const int w0 = 16 * s + 4 * (l >> 4);
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    if (n < N && w0 + 4 <= wpr) v = *reinterpret_cast<const u32x4_t*>(q + (size_t)n * wpr + w0);
+    codes[idx] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void prep_planes_kernel(const uint16_t* __restrict__ lut, int N, int ng, int T,
+                                                          u32x4_t* __restrict__ planes) {
+  const size_t total = (size_t)T * ng * 32;
+  for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
+    const int rr = (int)(idx & 15);
+    const int p = (int)((idx >> 4) & 1);
+    const size_t tg = idx >> 5;
+    const int g = (int)(tg % (size_t)ng);
+    const int t = (int)(tg / (size_t)ng);
+    const int n = 16 * t + rr;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (n < N) {
+      const uint16_t* e = lut + ((size_t)n * ng + g) * 16;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const uint32_t b = p ? (uint32_t)(e[k] >> 8) : (uint32_t)(e[k] & 0xFFu);
+        w[k >> 2] |= b << (8 * (k & 3));
+      }
+    }
+    planes[idx] = u32x4_t{w[0], w[1], w[2], w[3]};
+  }
+}
+
+// One thread per (row, chunk): the chunk's entries get their column and delta.
+__global__ __launch_bounds__(256) void prep_outliers_kernel(const uint32_t* __restrict__ q,
+                                                            const uint16_t* __restrict__ lut,
+                                                            const int32_t* __restrict__ offsets,
+                                                            const uint16_t* __restrict__ cols,
+                                                            const uint8_t* __restrict__ vals, int N, int K, int wpr,
+                                                            int ng, int G, int nch, uint16_t* __restrict__ gcol,
+                                                            float* __restrict__ delta) {
+  const size_t total = (size_t)N * nch;
+  for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
+    const int n = (int)(idx / (size_t)nch);
+    const int c = (int)(idx - (size_t)n * nch);
+    const int32_t* offr = offsets + (size_t)n * (nch + 1);
+    const int e_lo = offr[c];
+    const int e_hi = offr[c + 1];
+    const uint32_t* qrow = q + (size_t)n * wpr;
+    for (int e = e_lo; e < e_hi; ++e) {
+      const int cl = (int)cols[e];
+      const int col = c * 512 + cl;
+      if (cl < 512 && col < K) {
+        const uint32_t code = (qrow[col >> 3] >> (4 * (col & 7))) & 15u;
+        const int g = G > 0 ? min(col / G, ng - 1) : 0;
+        const float w_true = h2f((uint16_t)((uint32_t)vals[e] << 8));
+        gcol[e] = (uint16_t)col;
+        delta[e] = w_true - h2f(lut[((size_t)n * ng + g) * 16 + code]);
+      } else {  // dropped (the reference drops col >= K; a chunk column >= 512 is malformed)
+        gcol[e] = (uint16_t)(c * 512);
+        delta[e] = 0.f;
+      }
+    }
+  }
+}
+
+template <bool PER_ROW, int TPB, int MB>
+hipError_t launch_tpl(const StreamArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((stream4_kernel<PER_ROW, TPB, MB>), grid, dim3(256), lds, stream, a);
+  return hipGetLastError();
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+}  // namespace
+
+// ------------------------------------------------------------------ host side
+
+bool prepared_supported(int N, int K, int bits, int group_size) {
+  if (bits != 4 || N <= 0 || K <= 0 || K % 8 != 0 || K > 65535) return false;
+  return group_size == 0 || group_size % 32 == 0;
+}
+
+PreparedLayout prepared_layout(int N, int K, int group_size, int64_t nnz) {
+  PreparedLayout p{};
+  p.T = (N + 15) / 16;
+  p.S = (K + 127) / 128;
+  p.ng = group_size > 0 ? (K + group_size - 1) / group_size : 1;
+  p.codes_off = 0;
+  p.planes_off = align256((size_t)p.T * p.S * 1024);
+  p.gcol_off = p.planes_off + align256((size_t)p.T * p.ng * 512);
+  p.delta_off = p.gcol_off + align256((size_t)nnz * 2);
+  p.bytes = p.delta_off + align256((size_t)nnz * 4);
+  return p;
+}
+
+hipError_t launch_prepare(const Layer& L, int64_t nnz, void* prepared, hipStream_t stream) {
+  const PreparedLayout p = prepared_layout(L.N, L.K, L.group_size, nnz);
+  char* base = reinterpret_cast<char*>(prepared);
+  auto grid_for = [](size_t total) { return dim3((unsigned)std::min<size_t>((total + 255) / 256, 65535)); };
+  const int ng = L.group_size > 0 ? L.ng : 1;
+  hipLaunchKernelGGL(prep_codes_kernel, grid_for((size_t)p.T * p.S * 64), dim3(256), 0, stream, L.q, L.N, L.wpr, p.T,
+                     p.S, reinterpret_cast<u32x4_t*>(base + p.codes_off));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(prep_planes_kernel, grid_for((size_t)p.T * ng * 32), dim3(256), 0, stream, L.lut, L.N, ng, p.T,
+                     reinterpret_cast<u32x4_t*>(base + p.planes_off));
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (L.offsets != nullptr && nnz > 0) {
+    hipLaunchKernelGGL(prep_outliers_kernel, grid_for((size_t)L.N * L.nch), dim3(256), 0, stream, L.q, L.lut,
+                       L.offsets, L.cols, L.vals, L.N, L.K, L.wpr, ng, L.group_size, L.nch,
+                       reinterpret_cast<uint16_t*>(base + p.gcol_off), reinterpret_cast<float*>(base + p.delta_off));
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank) {
+  StreamPlan p{};
+  const int T = (N + 15) / 16;
+  const int nch = (K + 511) / 512;
+  p.tpb = M <= 2 ? 1 : 4;
+  const int TB = (T + p.tpb - 1) / p.tpb;
+  const int target = kBlocksPerCU * std::max(1, cu_count);
+  int splits = std::max(1, std::min(nch, (target + TB - 1) / TB));
+  int cps = (nch + splits - 1) / splits;
+  const int cps_max = std::max(1, kXBudget / (M * 1024));
+  cps = std::min(cps, cps_max);
+  splits = (nch + cps - 1) / cps;
+  p.splits = splits;
+  p.cps = cps;
+  p.TB = TB;
+  p.h_blocks = fused_rank > 0 ? (K + kHCols - 1) / kHCols : 0;
+  const size_t hf = fused_rank > 0 ? align256((size_t)M * fused_rank * 4) : 0;
+  const size_t hp = fused_rank > 0 ? align256((size_t)p.h_blocks * M * fused_rank * 4) : 0;
+  const size_t part = splits > 1 ? (size_t)splits * M * N * 4 : 0;
+  p.hfin_off = 0;
+  p.hpart_off = hf;
+  p.partial_off = hf + hp;
+  p.workspace_bytes = hf + hp + part;
+  p.ok = M >= 1 && M <= stream_max_m() && (splits == 1 || TB <= (int)(kSyncBytes / 4) - kSyncTile) &&
+         fused_rank % 8 == 0 && fused_rank <= kMaxRank;
+  return p;
+}
+
+int stream_max_m() { return 8; }
+int stream_max_rank() { return kMaxRank; }
+
+hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, const Dora& D, const uint16_t* x,
+                         uint16_t* out, int M, const StreamPlan& plan, float* workspace, uint32_t* sync,
+                         hipStream_t stream) {
+  const PreparedLayout lay = prepared_layout(L.N, L.K, L.group_size, nnz);
+  const char* base = reinterpret_cast<const char*>(prepared);
+  StreamArgs a{};
+  a.codes = reinterpret_cast<const u32x4_t*>(base + lay.codes_off);
+  a.planes = reinterpret_cast<const u32x4_t*>(base + lay.planes_off);
+  const bool csr = L.offsets != nullptr && nnz > 0;
+  a.gcol = reinterpret_cast<const uint16_t*>(base + lay.gcol_off);
+  a.delta = reinterpret_cast<const float*>(base + lay.delta_off);
+  a.offsets = csr ? L.offsets : nullptr;
+  a.x = x;
+  a.out = out;
+  a.B = D.B;
+  a.H = D.H;
+  a.gamma = D.gamma;
+  a.A = D.A;
+  a.scale = D.scale;
+  a.r = D.r;
+  a.M = M;
+  a.N = L.N;
+  a.K = L.K;
+  a.S = lay.S;
+  a.ng = lay.ng;
+  a.nch = (L.K + 511) / 512;
+  a.T = lay.T;
+  a.TB = plan.TB;
+  a.g_magic = L.group_size > 0 ? (uint32_t)((0x100000000ull / (uint64_t)L.group_size) + 1ull) : 0u;
+  a.splits = plan.splits;
+  a.cps = plan.cps;
+  a.xstride = plan.cps * 512 + 8;
+  const bool fused_h = D.r > 0 && D.H == nullptr;
+  a.h_blocks = fused_h ? plan.h_blocks : 0;
+  char* ws = reinterpret_cast<char*>(workspace);
+  a.hfin = reinterpret_cast<float*>(ws + plan.hfin_off);
+  a.hpart = reinterpret_cast<float*>(ws + plan.hpart_off);
+  a.partial = reinterpret_cast<float*>(ws + plan.partial_off);
+  a.sync = sync;
+  const int rows = 16 * plan.tpb;
+  const int mb = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+  size_t lds = (((size_t)M * a.xstride * 2 + 15) & ~(size_t)15) + 64 + 4 * 256 * 4 + (size_t)mb * rows * 4 +
+               (size_t)M * std::max(D.r, 1) * 4 + (size_t)rows * D.r * 2 + (size_t)rows * 2;
+  if (fused_h) lds = std::max(lds, (size_t)4 * (kMaxRank / 16) * 4 * 64 * 4);
+  const dim3 grid(a.h_blocks + plan.TB * plan.splits);
+  const bool per_row = L.group_size <= 0 || lay.ng == 1;
+  if (per_row) a.ng = 1;
+#define WLQ_STREAM_DISPATCH(PR)                                                  \
+  if (plan.tpb == 1) {                                                          \
+    if (mb == 1) return launch_tpl<PR, 1, 1>(a, grid, lds, stream);             \
+    return launch_tpl<PR, 1, 2>(a, grid, lds, stream);                          \
+  }                                                                             \
+  if (mb <= 4) return launch_tpl<PR, 4, 4>(a, grid, lds, stream);               \
+  return launch_tpl<PR, 4, 8>(a, grid, lds, stream);
+  if (per_row) {
+    WLQ_STREAM_DISPATCH(true)
+  } else {
+    WLQ_STREAM_DISPATCH(false)
+  }
+#undef WLQ_STREAM_DISPATCH
+}
+
+}  // namespace wlq

@@ -3,9 +3,11 @@
 Registers the custom ops ``torch.ops.wlq_fastShot.gemv`` and ``.gemm`` with the
 reference's schemas (vllm_wlq/__init__.py:9-74) -- ``out`` is mutated in place,
 fake implementations keep them traceable for graph capture and torch.compile --
-plus trailing defaulted arguments: ``group_size`` (0 = one LUT per row) and
+plus trailing defaulted arguments: ``group_size`` (0 = one LUT per row),
 ``lora_A`` (when lora_h / lora_H is None, the op computes the DoRA H itself as
-fp32(fp16(x @ lora_A^T)), the reference caller's F.linear).
+fp32(fp16(x @ lora_A^T)), the reference caller's F.linear) and ``prepared``
+(the layer's load-time tile-contiguous layout from ``_C.prepare_layer``, used by
+the decode kernel for up to 8 activation rows).
 Both call the ``_C`` extension, which calls the C ABI of ``libwlq_hip.so``.
 """
 from __future__ import annotations
@@ -40,13 +42,15 @@ def _register_ops() -> None:
         lora_scale: float = 1.0,
         group_size: int = 0,
         lora_A: Optional[torch.Tensor] = None,
+        prepared: Optional[torch.Tensor] = None,
     ) -> None:
         _C.gemv_forward(q_packed, lut_c, x, out, int(N), int(K), int(bits), chunk_offsets, chunk_cols, chunk_vals,
-                        lora_B, lora_h, dora_gamma, float(lora_scale), int(group_size), lora_A)
+                        lora_B, lora_h, dora_gamma, float(lora_scale), int(group_size), lora_A, prepared)
 
     @_gemv_op.register_fake
     def _gemv_fake(q_packed, lut_c, x, out, N, K, bits, chunk_offsets=None, chunk_cols=None, chunk_vals=None,
-                   lora_B=None, lora_h=None, dora_gamma=None, lora_scale=1.0, group_size=0, lora_A=None):
+                   lora_B=None, lora_h=None, dora_gamma=None, lora_scale=1.0, group_size=0, lora_A=None,
+                   prepared=None):
         return None
 
     @torch.library.custom_op(f"{ns}::gemm", mutates_args={"out"})
@@ -68,14 +72,16 @@ def _register_ops() -> None:
         lora_scale: float = 1.0,
         group_size: int = 0,
         lora_A: Optional[torch.Tensor] = None,
+        prepared: Optional[torch.Tensor] = None,
     ) -> None:
         _C.gemm_forward(X, q_packed, lut_c, out, int(N), int(K), int(bits), int(words_per_row), chunk_offsets,
-                        chunk_cols, chunk_vals, lora_H, lora_B, dora_gamma, float(lora_scale), int(group_size), lora_A)
+                        chunk_cols, chunk_vals, lora_H, lora_B, dora_gamma, float(lora_scale), int(group_size), lora_A,
+                        prepared)
 
     @_gemm_op.register_fake
     def _gemm_fake(X, q_packed, lut_c, out, N, K, bits, words_per_row, chunk_offsets=None, chunk_cols=None,
                    chunk_vals=None, lora_H=None, lora_B=None, dora_gamma=None, lora_scale=1.0, group_size=0,
-                   lora_A=None):
+                   lora_A=None, prepared=None):
         return None
 
 

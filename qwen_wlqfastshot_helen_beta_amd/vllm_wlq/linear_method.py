@@ -371,6 +371,7 @@ class WLQLinearMethod(LinearMethodBase):
         layer.lora_B = B16
         layer.dora_gamma = gamma
         layer.lora_scale = scale
+        layer.wlq_prepared = prepare_layer(layer)
         if layer.N > WLQLinearMethod._MAX_N or layer.K > WLQLinearMethod._MAX_K:
             WLQLinearMethod._MAX_N = max(WLQLinearMethod._MAX_N, layer.N)
             WLQLinearMethod._MAX_K = max(WLQLinearMethod._MAX_K, layer.K)
@@ -432,22 +433,23 @@ class WLQLinearMethod(LinearMethodBase):
         gs = int(getattr(layer, "wlq_group_size", 0))
         scale = float(getattr(layer, "lora_scale", 1.0))
         A = layer.lora_A_f16 if has_dora else None
+        prep = getattr(layer, "wlq_prepared", None)
         if M == 1:
             # H = fp32(fp16(x A^T)) is computed inside the product from lora_A
             torch.ops.wlq_fastShot.gemv(layer.q_packed_aligned, layer.lut_c, x2.squeeze(0), out.squeeze(0), layer.N,
                                         layer.K, bits, layer.chunk_offsets, layer.chunk_cols, layer.chunk_vals,
-                                        lora_B, None, gamma, scale, gs, A)
+                                        lora_B, None, gamma, scale, gs, A, prep)
         else:
             torch.ops.wlq_fastShot.gemm(x2, layer.q_packed_aligned, layer.lut_c, out, layer.N, layer.K, bits,
                                         layer.words_per_row, layer.chunk_offsets, layer.chunk_cols, layer.chunk_vals,
-                                        None, lora_B, gamma, scale, gs, A)
+                                        None, lora_B, gamma, scale, gs, A, prep)
         y = out if orig_dtype == torch.float16 else out.to(orig_dtype)
         if bias is not None:
             y.add_(bias)
         return y.view(*orig_shape[:-1], layer.N)
 
 
-def attach_synthetic(layer: torch.nn.Module, synth, device) -> torch.nn.Module:
+def attach_synthetic(layer: torch.nn.Module, synth, device, prepared: bool = True) -> torch.nn.Module:
     """Put a ``synth.SynthLayer`` onto ``layer`` in the post-load device format
     (what process_weights_after_loading produces), for benchmarks and tests."""
     t = synth.to_torch(device)
@@ -465,4 +467,16 @@ def attach_synthetic(layer: torch.nn.Module, synth, device) -> torch.nn.Module:
     layer.lora_B = t.get("lora_B")
     layer.dora_gamma = t.get("dora_gamma")
     layer.lora_scale = synth.lora_scale
+    layer.wlq_prepared = prepare_layer(layer) if prepared else None
     return layer
+
+
+def prepare_layer(layer: torch.nn.Module) -> Optional[torch.Tensor]:
+    """The layer's load-time tile-contiguous layout for the decode kernel (None when
+    its format has none: only 4-bit codes with a per-row LUT or a group size that is
+    a multiple of 32).  Built on the device from the reference-format tensors, which
+    the layer keeps for the other kernels and for dequant_w0."""
+    t = _C.prepare_layer(layer.q_packed_aligned, layer.lut_c, layer.N, layer.K, int(layer.quant_bits),
+                         int(getattr(layer, "wlq_group_size", 0)), layer.chunk_offsets, layer.chunk_cols,
+                         layer.chunk_vals)
+    return t if t.numel() > 0 else None

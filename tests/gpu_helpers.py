@@ -94,3 +94,80 @@ def oracle_product(L: synth.SynthLayer, x: np.ndarray, H, with_csr: bool = True,
     if H is None:
         return O.linear_forward(x, W0, round_gemm_output=round_gemm_output)
     return O.linear_forward(x, W0, H, L.B, L.gamma, L.lora_scale, round_gemm_output=round_gemm_output)
+
+
+def prepared_reference(L: synth.SynthLayer):
+    """numpy rebuild of the prepared (tile-contiguous) layout from the reference-format
+    arrays: (codes u32 [T, S, 64, 4], planes u8 [T, ng, 2, 16, 16], gcol, delta).
+    Codes: lane l = r + 16 kq of tile t, slab s holds words 16 s + 4 kq .. +3 of row
+    16 t + r; planes: low / high bytes of the 16 LUT entries of row 16 t + r, group g;
+    gcol / delta: the oracle's outlier_delta."""
+    N, K = L.N, L.K
+    T, S = -(-N // 16), -(-K // 128)
+    ng = 1 if L.group_size <= 0 or L.group_size >= K else -(-K // L.group_size)
+    q = L.q.view(np.uint32).reshape(N, L.wpr)
+    qpad = np.zeros((T * 16, S * 16), dtype=np.uint32)
+    qpad[:N, :L.wpr] = q
+    codes = qpad.reshape(T, 16, S, 4, 4).transpose(0, 2, 3, 1, 4).reshape(T, S, 64, 4)
+    lut = L.lut.view(np.uint16).reshape(N, ng, 16)
+    lpad = np.zeros((T * 16, ng, 16), dtype=np.uint16)
+    lpad[:N] = lut
+    planes = np.stack([(lpad & 0xFF).astype(np.uint8), (lpad >> 8).astype(np.uint8)], axis=2)  # [T*16, ng, 2, 16]
+    planes = planes.reshape(T, 16, ng, 2, 16).transpose(0, 2, 3, 1, 4)
+    gs = 0 if ng == 1 else L.group_size
+    gcol, delta = O.outlier_delta(L.q, L.lut, N, K, L.bits, L.offsets, L.cols, L.vals, group_size=gs)
+    return codes, planes, gcol, delta
+
+
+def split_prepared(buf: np.ndarray, L: synth.SynthLayer):
+    """Cut a prepared buffer (uint8) into its four parts (offsets as documented in
+    include/wlq_abi.h: 256-byte aligned, codes | planes | gcol | delta)."""
+    N, K = L.N, L.K
+    T, S = -(-N // 16), -(-K // 128)
+    ng = 1 if L.group_size <= 0 or L.group_size >= K else -(-K // L.group_size)
+    a = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    o_pl = a(T * S * 1024)
+    o_gc = o_pl + a(T * ng * 512)
+    o_dl = o_gc + a(L.nnz * 2)
+    codes = buf[:T * S * 1024].view(np.uint32).reshape(T, S, 64, 4)
+    planes = buf[o_pl:o_pl + T * ng * 512].reshape(T, ng, 2, 16, 16)
+    gcol = buf[o_gc:o_gc + L.nnz * 2].view(np.uint16)
+    delta = buf[o_dl:o_dl + L.nnz * 4].view(np.float32)
+    return codes, planes, gcol, delta
+
+
+def run_prepared(vw, L: synth.SynthLayer, x: np.ndarray, dora: str = "fused", with_csr: bool = True, prep=None,
+                 t=None):
+    """Product through the torch ops with the layer's prepared layout.
+    dora: "fused" (lora_A given, H computed in the kernel), "h" (H given), "none".
+    Returns (y fp16 numpy, H used by the oracle or None)."""
+    t = t or L.to_torch(DEV)
+    if prep is None:
+        prep = vw._C.prepare_layer(t["q_packed"], t["lut_c"], L.N, L.K, L.bits, L.group_size,
+                                   t["chunk_offsets"] if with_csr else None, t["chunk_cols"] if with_csr else None,
+                                   t["chunk_vals"] if with_csr else None)
+    xt = torch.from_numpy(x).to(DEV)
+    M = x.shape[0]
+    use = dora != "none" and L.B is not None
+    H = None
+    Hor = None
+    if use and dora == "h":
+        H = torch.nn.functional.linear(xt, t["lora_A"]).float()
+        Hor = H.cpu().numpy()
+    elif use:
+        Hor = O.lora_h(x, L.A)
+    A = t["lora_A"] if use and dora == "fused" else None
+    off = t["chunk_offsets"] if with_csr else None
+    cols = t["chunk_cols"] if with_csr else None
+    vals = t["chunk_vals"] if with_csr else None
+    out = torch.empty((M, L.N), dtype=torch.float16, device=DEV)
+    B = t.get("lora_B") if use else None
+    g = t.get("dora_gamma") if use else None
+    if M == 1:
+        torch.ops.wlq_fastShot.gemv(t["q_packed"], t["lut_c"], xt[0], out[0], L.N, L.K, L.bits, off, cols, vals, B,
+                                    H[0] if H is not None else None, g, L.lora_scale, L.group_size, A, prep)
+    else:
+        torch.ops.wlq_fastShot.gemm(xt, t["q_packed"], t["lut_c"], out, L.N, L.K, L.bits, L.wpr, off, cols, vals, H,
+                                    B, g, L.lora_scale, L.group_size, A, prep)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), Hor

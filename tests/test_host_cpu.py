@@ -107,8 +107,24 @@ def test_abi_exports_every_declared_symbol():
     assert len(names) >= 12
     for n in names:
         assert hasattr(lib, n), f"libwlq_hip.so does not export {n}"
-    assert lib.wlq_abi_version() == 3
+    assert lib.wlq_abi_version() == 4
     assert lib.wlq_status_string(4) == b"WLQ_ERR_CAPACITY" or b"capacity" in lib.wlq_status_string(4).lower()
+
+
+def test_abi_prepared_bytes():
+    """Size of the prepared layout (host query, no GPU): 256-byte aligned parts
+    codes | planes | gcol | delta; 0 for formats without one."""
+    lib = load_abi()
+    a = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    for N, K, G, nnz in ((37888, 3584, 128, 678960), (77, 1000, 32, 100), (16, 512, 0, 0), (5, 8, 128, 1)):
+        T, S = -(-N // 16), -(-K // 128)
+        ng = 1 if G == 0 or G >= K else -(-K // G)
+        want = a(T * S * 1024) + a(T * ng * 512) + a(nnz * 2) + a(nnz * 4)
+        assert lib.wlq_prepared_bytes(N, K, 4, G, nnz) == want, (N, K, G)
+    assert lib.wlq_prepared_bytes(64, 640, 3, 64, 0) == 0     # 3-bit
+    assert lib.wlq_prepared_bytes(64, 960, 4, 48, 0) == 0     # group not a multiple of 32
+    assert lib.wlq_prepared_bytes(64, 1001, 4, 128, 0) == 0   # K % 8 != 0
+    assert lib.wlq_prepared_bytes(64, 70000, 4, 128, 0) == 0  # columns beyond 16 bits
 
 
 def test_abi_host_helpers_match_oracle():
@@ -199,15 +215,17 @@ def test_op_schemas_match_reference():
                            "SymInt K, SymInt bits, SymInt words_per_row, Tensor? chunk_offsets"), gemm
     # lora_H before lora_B in gemm (reference order), trailing defaulted extensions only
     assert gemm.index("lora_H") < gemm.index("lora_B")
-    assert gemv.endswith("float lora_scale=1., SymInt group_size=0, Tensor? lora_A=None) -> ()")
-    assert gemm.endswith("float lora_scale=1., SymInt group_size=0, Tensor? lora_A=None) -> ()")
+    assert gemv.endswith("float lora_scale=1., SymInt group_size=0, Tensor? lora_A=None, "
+                         "Tensor? prepared=None) -> ()")
+    assert gemm.endswith("float lora_scale=1., SymInt group_size=0, Tensor? lora_A=None, "
+                         "Tensor? prepared=None) -> ()")
 
 
 def test_c_extension_functions():
     from qwen_wlqfastshot_helen_beta_amd.vllm_wlq import _C
 
     for name in ("gemv_forward", "gemm_forward", "dequant_w0", "init_workspaces", "decode_ef_to_chunk_csr",
-                 "repack_q_indices_row_aligned"):
+                 "repack_q_indices_row_aligned", "prepare_layer"):
         assert hasattr(_C, name), name
     doc = _C.dequant_w0.__doc__
     for arg in ("q_packed", "lut_c", "W_out", "N", "K", "bits", "words_per_row", "chunk_offsets", "chunk_cols",

@@ -212,6 +212,48 @@ def test_dequant_groups_loops_and_outliers():
     assert np.array_equal(W1.view(np.uint16), W0.view(np.uint16))
 
 
+def test_outlier_delta_hand():
+    lut = np.array([i * 0.25 - 2.0 for i in range(16)], dtype=np.float16)[None, :]  # -2.0 .. 1.75
+    codes = np.array([[0, 15, 3, 8, 1, 2, 9, 10, 4, 5]], dtype=np.uint8)
+    q, _ = O.pack_row_aligned(codes, 4)
+    off = np.array([[0, 3]], dtype=np.int32)
+    cols = np.array([3, 9, 11], dtype=np.uint16)  # column 11 is past K = 10: dropped
+    vals = np.array([0x3C, 0xC1, 0x3C], dtype=np.uint8)  # 1.0, -2.5, 1.0
+    gcol, delta = O.outlier_delta(q, lut, 1, 10, 4, off, cols, vals)
+    assert gcol.tolist() == [3, 9, 0]
+    # code 8 -> 0.0, code 5 -> -0.75
+    assert delta.tolist() == [1.0, -1.75, 0.0]
+
+
+def test_outlier_delta_loops_and_invariant():
+    rng = np.random.default_rng(8)
+    N, K, G, bits = 5, 1100, 64, 4
+    codes = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    lut = _lut_rows(N, -(-K // G), bits, 3)
+    q, _ = O.pack_row_aligned(codes, bits)
+    mask = rng.random((N, K)) < 0.03
+    vals = (rng.standard_normal(mask.sum()) * 0.2).astype(np.float16)
+    off, cols, v = O.build_chunk_csr(mask, vals, 512)
+    gcol, delta = O.outlier_delta(q, lut, N, K, bits, off, cols, v, group_size=G)
+    e = 0
+    for n in range(N):
+        for k in range(K):
+            if mask[n, k]:
+                w_true = np.float32((v[e].astype(np.uint16) << 8).view(np.float16))
+                w_lut = np.float32(lut[n, k // G, codes[n, k]])
+                assert gcol[e] == k
+                assert delta[e] == np.float32(w_true - w_lut)
+                e += 1
+    # sum of delta * x over a row's entries == (W0 - W_lut) . x
+    x = rng.standard_normal(K)
+    W0 = O.dequant(q, lut, N, K, bits, off, cols, v, group_size=G).astype(np.float64)
+    Wl = O.dequant(q, lut, N, K, bits, group_size=G).astype(np.float64)
+    _, rows, _ = O.csr_to_coo(off, cols, 512)
+    corr = np.zeros(N)
+    np.add.at(corr, rows, delta.astype(np.float64) * x[gcol])
+    assert np.allclose(corr, (W0 - Wl) @ x, rtol=1e-6, atol=1e-6)
+
+
 # ---------------------------------------------------------------- Elias-Fano
 
 def test_ef_hand_bitstream():
