@@ -1,10 +1,11 @@
-// Decode product on the prepared (tile-contiguous) layout: M = 1..8 activation
+// Decode product on the prepared (tile-contiguous) layout: M = 1..32 activation
 // rows, 4-bit codes, per-row LUTs or LUT groups of a multiple of 32 columns.
 //
 // Reference behaviour replaced: gemv_chunk_csr_kernel + launch_gemv_chunk_csr
 // (csrc/gemv_kernel.cu:86-320, :396-457) and the split-K reduce
 // (csrc/gemv_kernel.cu:322-353) for M == 1, gemm_metalog_dora_kernel
-// (csrc/gemm_kernel.cu:32-294) for 2 <= M < 16.  Same arithmetic: W0 rows
+// (csrc/gemm_kernel.cu:32-294) for 2 <= M < 16, and the dequant -> GEMM -> DoRA
+// epilogue sequence (csrc/vllm_binding.cpp:355-393) for 16 <= M <= 32.  Same arithmetic: W0 rows
 // expanded through their LUTs, the delta-form outlier correction
 // (w_true - lut[code]) * x (csrc/gemv_kernel.cu:262-288), the DoRA epilogue
 // fp16_rn((acc + s * h.B) * gamma) (csrc/gemv_kernel.cu:305-319).
@@ -122,9 +123,11 @@ __device__ __forceinline__ int group_of(int col, uint32_t magic) { return (int)_
 // ------------------------------------------------------------------ DoRA blocks
 
 // hpart[hb, i, j] = sum over columns [512 hb, +512) of x[i, k] * A[j, k]; wave w
-// covers 128 columns with MFMA 16x16x32 (A = activation rows, B = lora_A rows,
-// both in natural column order); the four wave sums are added through LDS.  The
-// block that arrives last rounds H = fp16(sum over hb) and publishes it.
+// covers 128 columns with MFMA 16x16x32 (A = 16 activation rows per group, NA
+// groups; B = lora_A rows; both in natural column order); the four wave sums are
+// added through LDS.  The block that arrives last rounds H = fp16(sum over hb) and
+// publishes it.
+template <int NA>
 __device__ void dora_block(const StreamArgs& a, int hb, float* red) {
   constexpr int JT = kMaxRank / 16;
   const int lane = threadIdx.x & 63;
@@ -132,16 +135,23 @@ __device__ void dora_block(const StreamArgs& a, int hb, float* red) {
   const int r16 = lane & 15;
   const int kq = lane >> 4;
   const int jt_n = (a.r + 15) >> 4;
-  float4_t acc[JT];
+  float4_t acc[NA][JT];
 #pragma unroll
-  for (int jt = 0; jt < JT; ++jt) acc[jt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < NA; ++g)
+#pragma unroll
+    for (int jt = 0; jt < JT; ++jt) acc[g][jt] = float4_t{0.f, 0.f, 0.f, 0.f};
   const int kbase = hb * kHCols + wave * 128;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int k = kbase + 32 * ks + 8 * kq;
     const bool kin = k < a.K;  // K % 8 == 0: an 8-column unit is all inside or all outside
-    u32x4_t xa = {0u, 0u, 0u, 0u};
-    if (r16 < a.M && kin) xa = *reinterpret_cast<const u32x4_t*>(a.x + (size_t)r16 * a.K + k);
+    u32x4_t xa[NA];
+#pragma unroll
+    for (int g = 0; g < NA; ++g) {
+      const int i = 16 * g + r16;
+      xa[g] = u32x4_t{0u, 0u, 0u, 0u};
+      if (i < a.M && kin) xa[g] = *reinterpret_cast<const u32x4_t*>(a.x + (size_t)i * a.K + k);
+    }
     u32x4_t ab[JT];
 #pragma unroll
     for (int jt = 0; jt < JT; ++jt) {
@@ -150,26 +160,31 @@ __device__ void dora_block(const StreamArgs& a, int hb, float* red) {
       if (jt < jt_n && j < a.r && kin) ab[jt] = *reinterpret_cast<const u32x4_t*>(a.A + (size_t)j * a.K + k);
     }
 #pragma unroll
-    for (int jt = 0; jt < JT; ++jt)
-      if (jt < jt_n) acc[jt] = mfma16x16x32(xa, ab[jt], acc[jt]);
+    for (int g = 0; g < NA; ++g)
+#pragma unroll
+      for (int jt = 0; jt < JT; ++jt)
+        if (jt < jt_n) acc[g][jt] = mfma16x16x32(xa[g], ab[jt], acc[g][jt]);
   }
-  // red[wave][jt][e][lane]
+  // red[wave][g][jt][e][lane]
 #pragma unroll
-  for (int jt = 0; jt < JT; ++jt)
-    if (jt < jt_n)
+  for (int g = 0; g < NA; ++g)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) red[((wave * JT + jt) * 4 + e) * 64 + lane] = acc[jt][e];
+    for (int jt = 0; jt < JT; ++jt)
+      if (jt < jt_n)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[(((wave * NA + g) * JT + jt) * 4 + e) * 64 + lane] = acc[g][jt][e];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < jt_n * 256; idx += blockDim.x) {
+  for (int idx = threadIdx.x; idx < NA * jt_n * 256; idx += blockDim.x) {
     const int ln = idx & 63;
     const int e = (idx >> 6) & 3;
-    const int jt = idx >> 8;
-    const int i = 4 * (ln >> 4) + e;
+    const int jt = (idx >> 8) % jt_n;
+    const int g = (idx >> 8) / jt_n;
+    const int i = 16 * g + 4 * (ln >> 4) + e;
     const int j = 16 * jt + (ln & 15);
     if (i < a.M && j < a.r) {
       float v = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) v += red[((w * JT + jt) * 4 + e) * 64 + ln];
+      for (int w = 0; w < 4; ++w) v += red[(((w * NA + g) * JT + jt) * 4 + e) * 64 + ln];
       store_dev(a.hpart + ((size_t)hb * a.M + i) * a.r + j, v);
     }
   }
@@ -212,16 +227,18 @@ __device__ __forceinline__ void wait_h_ready(const uint32_t* slot) {
 }
 
 template <bool PER_ROW, int TPB, int MB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WLQ_STREAM_WAVES_PER_EU)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MB > 16 ? 4 : WLQ_STREAM_WAVES_PER_EU)))
 void stream4_kernel(const StreamArgs a) {
   constexpr int WPT = 4 / TPB;       // waves per row tile
   constexpr int ROWS = 16 * TPB;     // output rows per block
   constexpr int TPR = 256 / ROWS;    // threads per row in the outlier pass
+  constexpr int NA = (MB + 15) / 16; // 16-row activation groups (MFMA A operands)
+  constexpr int XR = MB > 16 ? 2 * kXR : kXR;  // 16-byte activation units per thread
   extern __shared__ __align__(16) uint16_t smem[];
 
   int bid = blockIdx.x;
   if (bid < a.h_blocks) {
-    dora_block(a, bid, reinterpret_cast<float*>(smem));
+    dora_block<NA>(a, bid, reinterpret_cast<float*>(smem));
     return;
   }
   bid -= a.h_blocks;
@@ -241,15 +258,15 @@ void stream4_kernel(const StreamArgs a) {
   const int nw = (s1 - s0 - ph + WPT - 1) / WPT;  // this wave's slabs (may be 0)
   const int s_last = min(s0 + ph + WPT * max(nw - 1, 0), s1 - 1);  // prefetch clamp (in range)
 
-  // LDS: [x: M rows x xstride halves][64 B zeros][red: 4 x 256 f32][corr: MB x ROWS f32][H: M x r f32]
-  //      [B rows: ROWS x r halves][gamma: ROWS halves]
+  // LDS: [x: M rows x xstride halves][64 B zeros][red: 4 x NA x 256 f32]
+  //      [B rows: ROWS x r halves][gamma: ROWS halves]; H (M x r f32) reuses the x rows
+  //      once the outlier pass has read them.
   uint16_t* xs = smem;
   const int xbytes = ((a.M * a.xstride * 2) + 15) & ~15;
   uint16_t* zline = reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(smem) + xbytes);
   float* red = reinterpret_cast<float*>(reinterpret_cast<char*>(zline) + 64);
-  float* cres = red + 4 * 256;
-  float* hs = cres + MB * ROWS;
-  uint16_t* bs = reinterpret_cast<uint16_t*>(hs + a.M * max(a.r, 1));
+  float* hs = reinterpret_cast<float*>(smem);
+  uint16_t* bs = reinterpret_cast<uint16_t*>(red + 4 * NA * 256);
   uint16_t* gs = bs + ROWS * a.r;
 
   // Outlier pass mapping: thread (rho, j) walks entries j, j + TPR, ... of block row rho.
@@ -267,9 +284,9 @@ void stream4_kernel(const StreamArgs a) {
   // Activations [s0*128, s1*128) of the M rows: loads now, LDS stores after the prefetch is issued.
   const int upr = (s1 - s0) * 16;  // 8-column units per row
   const int total = a.M * upr;
-  u32x4_t xv[kXR];
+  u32x4_t xv[XR];
 #pragma unroll
-  for (int k = 0; k < kXR; ++k) {
+  for (int k = 0; k < XR; ++k) {
     const int u = min((int)threadIdx.x + 256 * k, max(total - 1, 0));
     const int i = u / upr;
     const int col = min(s0 * 128 + ((u - i * upr) << 3), a.K - 8);
@@ -314,7 +331,7 @@ void stream4_kernel(const StreamArgs a) {
   for (int u = 0; u < kPF; ++u) load_slab(buf[u], min(s0 + ph + WPT * u, s_last));
 
 #pragma unroll
-  for (int k = 0; k < kXR; ++k) {
+  for (int k = 0; k < XR; ++k) {
     const int u = (int)threadIdx.x + 256 * k;
     if (u < total) {
       const int i = u / upr;
@@ -347,9 +364,12 @@ void stream4_kernel(const StreamArgs a) {
   }
   __syncthreads();
 
-  // Slab loop.
-  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+  // Slab loop.  acc[g]: activation rows 16 g .. 16 g + 15.
+  float4_t acc[NA];
+#pragma unroll
+  for (int g = 0; g < NA; ++g) acc[g] = float4_t{0.f, 0.f, 0.f, 0.f};
   const uint16_t* xrow = (r < a.M) ? xs + r * a.xstride + kq * 32 : nullptr;
+  const uint16_t* xrow2 = (NA > 1 && r + 16 < a.M) ? xs + (r + 16) * a.xstride + kq * 32 : nullptr;
   auto consume = [&](const Slab& sl, int s) __attribute__((always_inline)) {
     LutPlanes<4> t4;
     if constexpr (PER_ROW) {
@@ -359,6 +379,7 @@ void stream4_kernel(const StreamArgs a) {
       t4.hi[0] = sl.hi.x; t4.hi[1] = sl.hi.y; t4.hi[2] = sl.hi.z; t4.hi[3] = sl.hi.w;
     }
     const uint16_t* xp = xrow ? xrow + (s - s0) * 128 : zline;
+    const uint16_t* xp2 = xrow2 ? xrow2 + (s - s0) * 128 : zline;
     const uint32_t w[4] = {sl.codes.x, sl.codes.y, sl.codes.z, sl.codes.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -366,7 +387,11 @@ void stream4_kernel(const StreamArgs a) {
       dequant_word4(w[q], t4, b);
       const u32x4_t bv = {b[0], b[1], b[2], b[3]};
       const u32x4_t av = *reinterpret_cast<const u32x4_t*>(xp + (xrow ? 8 * q : 0));
-      acc = mfma16x16x32(av, bv, acc);
+      acc[0] = mfma16x16x32(av, bv, acc[0]);
+      if constexpr (NA > 1) {
+        const u32x4_t av2 = *reinterpret_cast<const u32x4_t*>(xp2 + (xrow2 ? 8 * q : 0));
+        acc[1] = mfma16x16x32(av2, bv, acc[1]);
+      }
     }
   };
   // Steady state: every slot consumed is reloaded kPF slabs ahead; then one round with
@@ -394,9 +419,11 @@ void stream4_kernel(const StreamArgs a) {
       if (j0 + u < nw) consume(buf[u], s0 + ph + WPT * (j0 + u));
   }
 
-  // Wave partials: red[wave][e][lane] = D[i = 4 kq + e][row r].
+  // Wave partials: red[wave][g][e][lane] = D[i = 16 g + 4 kq + e][row r].
 #pragma unroll
-  for (int e = 0; e < 4; ++e) red[(wave * 4 + e) * 64 + lane] = acc[e];
+  for (int g = 0; g < NA; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[((wave * NA + g) * 4 + e) * 64 + lane] = acc[g][e];
 
   // Outliers: corr[i] = sum over the thread's entries of delta * x[i, col].
   float corr[MB];
@@ -424,15 +451,32 @@ void stream4_kernel(const StreamArgs a) {
         corr[i] = v;
       }
     }
-    if (jr == 0) {
-#pragma unroll
-      for (int i = 0; i < MB; ++i)
-        if (i < a.M) cres[i * ROWS + rho] = corr[i];
-    }
   }
   __syncthreads();
 
-  // Block sums for the outputs (i, rho): wave partials in phase order, then the outliers.
+  // Wave partial of output (i, row rr) in phase p.
+  auto red_at = [&](int i, int rr, int p) __attribute__((always_inline)) -> float& {
+    const int ln = (rr & 15) + 16 * ((i & 15) >> 2);
+    return red[((((rr >> 4) * WPT + p) * NA + (i >> 4)) * 4 + (i & 3)) * 64 + ln];
+  };
+  // The outlier sum of (i, rho), which every thread of the row's group holds after the
+  // butterfly, is added by thread jr = i % TPR into the last phase's partial.
+  if (csr) {
+#pragma unroll
+    for (int q = 0; q < (MB + TPR - 1) / TPR; ++q) {
+      const int i = q * TPR + jr;
+      if (i < a.M) {
+        float c = 0.f;
+#pragma unroll
+        for (int u = 0; u < TPR; ++u)
+          if (q * TPR + u < MB && u == jr) c = corr[min(q * TPR + u, MB - 1)];
+        red_at(i, rho, WPT - 1) += c;
+      }
+    }
+    __syncthreads();
+  }
+
+  // Block sums for the outputs (i, rr), o = i * ROWS + rr: wave partials in phase order.
   const int nouts = a.M * ROWS;
   constexpr int kOPT = (MB * ROWS + 255) / 256;  // outputs per thread
   float v[kOPT];
@@ -443,12 +487,9 @@ void stream4_kernel(const StreamArgs a) {
     if (o < nouts) {
       const int i = o / ROWS;
       const int rr = o - i * ROWS;
-      const int tl = rr >> 4;
-      const int ln = (rr & 15) + 16 * (i >> 2);
       float s = 0.f;
 #pragma unroll
-      for (int p = 0; p < WPT; ++p) s += red[((tl * WPT + p) * 4 + (i & 3)) * 64 + ln];
-      if (csr) s += cres[i * ROWS + rr];
+      for (int p = 0; p < WPT; ++p) s += red_at(i, rr, p);
       v[q] = s;
     }
   }
@@ -470,18 +511,31 @@ void stream4_kernel(const StreamArgs a) {
     __syncthreads();
     if (!s_last) return;
     compiler_fence();
+    // Sum the split partials in split order, kSumBatch splits of every output in flight at once
+    // (clamped addresses; the sums take only splits < a.splits).
+    constexpr int kSumBatch = 8;
+    size_t base[kOPT];
 #pragma unroll
     for (int q = 0; q < kOPT; ++q) {
-      const int o = (int)threadIdx.x + 256 * q;
-      if (o < nouts) {
-        const int i = o / ROWS;
-        const int n = tb * ROWS + (o - i * ROWS);
-        if (n < a.N) {
-          float s = 0.f;
-          for (int sp = 0; sp < a.splits; ++sp) s += load_dev(a.partial + ((size_t)sp * a.M + i) * a.N + n);
-          v[q] = s;
-        }
-      }
+      const int o = min((int)threadIdx.x + 256 * q, nouts - 1);
+      const int i = o / ROWS;
+      const int n = min(tb * ROWS + (o - i * ROWS), a.N - 1);
+      base[q] = (size_t)i * a.N + n;
+      v[q] = 0.f;
+    }
+    const size_t sstride = (size_t)a.M * a.N;
+    for (int sp0 = 0; sp0 < a.splits; sp0 += kSumBatch) {
+      float t[kOPT][kSumBatch];
+#pragma unroll
+      for (int q = 0; q < kOPT; ++q)
+#pragma unroll
+        for (int u = 0; u < kSumBatch; ++u)
+          t[q][u] = load_dev(a.partial + (size_t)min(sp0 + u, a.splits - 1) * sstride + base[q]);
+#pragma unroll
+      for (int q = 0; q < kOPT; ++q)
+#pragma unroll
+        for (int u = 0; u < kSumBatch; ++u)
+          if (sp0 + u < a.splits) v[q] += t[q][u];
     }
     if (threadIdx.x == 0) store_dev(a.sync + kSyncTile + tb, 0u);
   }
@@ -490,12 +544,19 @@ void stream4_kernel(const StreamArgs a) {
   const int slots = min(a.TB, kMaxSlots);
   uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
   if (a.r > 0) {
+    constexpr int kHB = 8;  // H words per thread in flight (M * r <= 32 * 64 = 8 * 256)
+    float hv[kHB];
     if (a.h_blocks > 0) {
       wait_h_ready(slot);
-      for (int idx = threadIdx.x; idx < a.M * a.r; idx += 256) hs[idx] = load_dev(a.hfin + idx);
+#pragma unroll
+      for (int u = 0; u < kHB; ++u) hv[u] = load_dev(a.hfin + min((int)threadIdx.x + 256 * u, a.M * a.r - 1));
     } else {
-      for (int idx = threadIdx.x; idx < a.M * a.r; idx += 256) hs[idx] = a.H[idx];
+#pragma unroll
+      for (int u = 0; u < kHB; ++u) hv[u] = a.H[min((int)threadIdx.x + 256 * u, a.M * a.r - 1)];
     }
+#pragma unroll
+    for (int u = 0; u < kHB; ++u)
+      if ((int)threadIdx.x + 256 * u < a.M * a.r) hs[threadIdx.x + 256 * u] = hv[u];
     __syncthreads();
   }
 #pragma unroll
@@ -691,7 +752,7 @@ StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank) {
   return p;
 }
 
-int stream_max_m() { return 8; }
+int stream_max_m() { return 32; }
 int stream_max_rank() { return kMaxRank; }
 
 hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, const Dora& D, const uint16_t* x,
@@ -734,10 +795,12 @@ hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, cons
   a.partial = reinterpret_cast<float*>(ws + plan.partial_off);
   a.sync = sync;
   const int rows = 16 * plan.tpb;
-  const int mb = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
-  size_t lds = (((size_t)M * a.xstride * 2 + 15) & ~(size_t)15) + 64 + 4 * 256 * 4 + (size_t)mb * rows * 4 +
-               (size_t)M * std::max(D.r, 1) * 4 + (size_t)rows * D.r * 2 + (size_t)rows * 2;
-  if (fused_h) lds = std::max(lds, (size_t)4 * (kMaxRank / 16) * 4 * 64 * 4);
+  const int mb = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : M <= 16 ? 16 : 32;
+  const int na = (mb + 15) / 16;
+  // the x rows (>= 1040 bytes per activation row) also hold H (<= 256 bytes per row) at the end
+  size_t lds = (((size_t)M * a.xstride * 2 + 15) & ~(size_t)15) + 64 + (size_t)4 * na * 256 * 4 +
+               (size_t)rows * D.r * 2 + (size_t)rows * 2;
+  if (fused_h) lds = std::max(lds, (size_t)4 * na * (kMaxRank / 16) * 4 * 64 * 4);
   const dim3 grid(a.h_blocks + plan.TB * plan.splits);
   const bool per_row = L.group_size <= 0 || lay.ng == 1;
   if (per_row) a.ng = 1;
@@ -747,7 +810,9 @@ hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, cons
     return launch_tpl<PR, 1, 2>(a, grid, lds, stream);                          \
   }                                                                             \
   if (mb <= 4) return launch_tpl<PR, 4, 4>(a, grid, lds, stream);               \
-  return launch_tpl<PR, 4, 8>(a, grid, lds, stream);
+  if (mb == 8) return launch_tpl<PR, 4, 8>(a, grid, lds, stream);               \
+  if (mb == 16) return launch_tpl<PR, 4, 16>(a, grid, lds, stream);             \
+  return launch_tpl<PR, 4, 32>(a, grid, lds, stream);
   if (per_row) {
     WLQ_STREAM_DISPATCH(true)
   } else {
