@@ -195,9 +195,17 @@ __device__ void dora_block(const StreamArgs& a, int hb, float* red) {
   __syncthreads();
   if (!s_last) return;
   compiler_fence();
+  // sums in block order, 8 blocks' partials in flight at once (clamped; only b < h_blocks added)
   for (int idx = threadIdx.x; idx < a.M * a.r; idx += blockDim.x) {
     float v = 0.f;
-    for (int b = 0; b < a.h_blocks; ++b) v += load_dev(a.hpart + (size_t)b * a.M * a.r + idx);
+    for (int b0 = 0; b0 < a.h_blocks; b0 += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = load_dev(a.hpart + (size_t)min(b0 + u, a.h_blocks - 1) * a.M * a.r + idx);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (b0 + u < a.h_blocks) v += t[u];
+    }
     store_dev(a.hfin + idx, h2f(f2h_rn(v)));  // the reference's F.linear output is fp16
   }
   stores_done();
@@ -214,17 +222,6 @@ struct Slab {
   u32x4_t codes;
   u32x4_t lo, hi;
 };
-
-// Waits until the block's ready slot is raised (bounded: a wait that never ends is
-// cut off after kSpinLimit polls rather than hang the GPU).
-__device__ __forceinline__ void wait_h_ready(const uint32_t* slot) {
-  if (threadIdx.x == 0) {
-    uint32_t spins = 0;
-    while (load_dev(slot) == 0u && ++spins < kSpinLimit) __builtin_amdgcn_s_sleep(2);
-  }
-  __syncthreads();
-  compiler_fence();
-}
 
 template <bool PER_ROW, int TPB, int MB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MB > 16 ? 4 : WLQ_STREAM_WAVES_PER_EU)))
@@ -425,6 +422,37 @@ void stream4_kernel(const StreamArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) red[((wave * NA + g) * 4 + e) * 64 + lane] = acc[g][e];
 
+  // DoRA H into registers.  A caller's H, or (one K split: this block finishes its rows) the
+  // computed H, is loaded now so the loads complete while the outlier pass runs; with several
+  // splits only the last to arrive needs H and loads it then.  Computed H: each wave first
+  // waits for the block's ready slot (normally raised long before; cut off after kSpinLimit
+  // polls rather than hang).  A block polls before it counts itself on the slot, so no slot is
+  // lowered while one of its tile blocks still polls.
+  const int slots = min(a.TB, kMaxSlots);
+  uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
+  constexpr int kHB = (MB * kMaxRank + 255) / 256;  // H words per thread (M * r <= MB * 64)
+  float hv[kHB];
+  auto load_h = [&]() __attribute__((always_inline)) {
+    if (a.h_blocks > 0) {
+      if (lane == 0) {
+        for (uint32_t spins = 0; load_dev(slot) == 0u && spins < kSpinLimit; ++spins) __builtin_amdgcn_s_sleep(2);
+      }
+      compiler_fence();
+#pragma unroll
+      for (int u = 0; u < kHB; ++u) hv[u] = load_dev(a.hfin + min((int)threadIdx.x + 256 * u, a.M * a.r - 1));
+    } else {
+#pragma unroll
+      for (int u = 0; u < kHB; ++u) hv[u] = a.H[min((int)threadIdx.x + 256 * u, a.M * a.r - 1)];
+    }
+  };
+  auto store_h = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kHB; ++u)
+      if ((int)threadIdx.x + 256 * u < a.M * a.r) hs[threadIdx.x + 256 * u] = hv[u];
+  };
+  const bool h_early = a.r > 0 && (a.splits == 1 || a.h_blocks == 0);
+  if (h_early) load_h();
+
   // Outliers: corr[i] = sum over the thread's entries of delta * x[i, col].
   float corr[MB];
 #pragma unroll
@@ -459,6 +487,8 @@ void stream4_kernel(const StreamArgs a) {
     const int ln = (rr & 15) + 16 * ((i & 15) >> 2);
     return red[((((rr >> 4) * WPT + p) * NA + (i >> 4)) * 4 + (i & 3)) * 64 + ln];
   };
+  // H over the x rows (read by the outlier pass above, so after its barrier).
+  if (h_early) store_h();
   // The outlier sum of (i, rho), which every thread of the row's group holds after the
   // butterfly, is added by thread jr = i % TPR into the last phase's partial.
   if (csr) {
@@ -473,8 +503,8 @@ void stream4_kernel(const StreamArgs a) {
         red_at(i, rho, WPT - 1) += c;
       }
     }
-    __syncthreads();
   }
+  if (csr || h_early) __syncthreads();
 
   // Block sums for the outputs (i, rr), o = i * ROWS + rr: wave partials in phase order.
   const int nouts = a.M * ROWS;
@@ -538,27 +568,14 @@ void stream4_kernel(const StreamArgs a) {
           if (sp0 + u < a.splits) v[q] += t[q][u];
     }
     if (threadIdx.x == 0) store_dev(a.sync + kSyncTile + tb, 0u);
+    if (a.r > 0 && !h_early) {  // the last split block: computed H now
+      load_h();
+      store_h();
+      __syncthreads();
+    }
   }
 
   // Epilogue: y = fp16_rn((v + s * H[i, :] . B[n, :]) * gamma[n]) with H, B and gamma from LDS.
-  const int slots = min(a.TB, kMaxSlots);
-  uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
-  if (a.r > 0) {
-    constexpr int kHB = 8;  // H words per thread in flight (M * r <= 32 * 64 = 8 * 256)
-    float hv[kHB];
-    if (a.h_blocks > 0) {
-      wait_h_ready(slot);
-#pragma unroll
-      for (int u = 0; u < kHB; ++u) hv[u] = load_dev(a.hfin + min((int)threadIdx.x + 256 * u, a.M * a.r - 1));
-    } else {
-#pragma unroll
-      for (int u = 0; u < kHB; ++u) hv[u] = a.H[min((int)threadIdx.x + 256 * u, a.M * a.r - 1)];
-    }
-#pragma unroll
-    for (int u = 0; u < kHB; ++u)
-      if ((int)threadIdx.x + 256 * u < a.M * a.r) hs[threadIdx.x + 256 * u] = hv[u];
-    __syncthreads();
-  }
 #pragma unroll
   for (int q = 0; q < kOPT; ++q) {
     const int o = (int)threadIdx.x + 256 * q;
