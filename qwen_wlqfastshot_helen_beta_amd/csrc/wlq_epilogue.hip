@@ -125,9 +125,13 @@ __device__ __forceinline__ u32x4_t load8z(const uint16_t* row, int k, int K, boo
 // H = fp16(X . A^T) for large M: a block owns a 16x16 tile of H (16 rows of X,
 // 16 columns of A^T); its 4 waves split K, each accumulating with MFMA
 // 16x16x32 (both operands in natural k order), and the partials meet in LDS.
-__global__ __launch_bounds__(256) void lora_h_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ A,
-                                                     int M, int K, int r, float* __restrict__ H, int vec) {
-  __shared__ float red[4][4][64];
+// H[M, r] = fp32(fp16(X . A^T)): one block per 16 x 16 tile of H, its 16 waves on K slices of a
+// multiple of 256 columns; each wave issues the 16 loads of 256 columns before their 8 MFMAs, so
+// a block needs about K / 4096 load round trips.  Wave sums are added through LDS in wave order.
+constexpr int kHWaves = 16;
+__global__ __launch_bounds__(1024) void lora_h_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ A,
+                                                      int M, int K, int r, float* __restrict__ H, int vec) {
+  __shared__ float red[kHWaves][4][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r16 = lane & 15;
@@ -139,19 +143,19 @@ __global__ __launch_bounds__(256) void lora_h_kernel(const uint16_t* __restrict_
   float4_t acc = {0.f, 0.f, 0.f, 0.f};
   const uint16_t* xr = X + (size_t)min(i, M - 1) * K;
   const uint16_t* ar = A + (size_t)min(j, r - 1) * K;
-  const int kslice = ((K + 3) / 4 + 127) / 128 * 128;
+  const int kslice = ((K + kHWaves - 1) / kHWaves + 255) / 256 * 256;
   const int kb = wave * kslice;
   const int ke = min(K, kb + kslice);
-  for (int k0 = kb; k0 < ke; k0 += 128) {
-    u32x4_t xa[4], ab[4];
+  for (int k0 = kb; k0 < ke; k0 += 256) {
+    u32x4_t xa[8], ab[8];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < 8; ++s) {
       const int k = k0 + 32 * s + 8 * kq;
       xa[s] = (i < M && k < ke) ? load8z(xr, k, ke, vec != 0) : u32x4_t{0u, 0u, 0u, 0u};
       ab[s] = (j < r && k < ke) ? load8z(ar, k, ke, vec != 0) : u32x4_t{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc = mfma16x16x32(xa[s], ab[s], acc);
+    for (int s = 0; s < 8; ++s) acc = mfma16x16x32(xa[s], ab[s], acc);
   }
 #pragma unroll
   for (int e = 0; e < 4; ++e) red[wave][e][lane] = acc[e];
@@ -159,7 +163,9 @@ __global__ __launch_bounds__(256) void lora_h_kernel(const uint16_t* __restrict_
   if (wave == 0) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float v = red[0][e][lane] + red[1][e][lane] + red[2][e][lane] + red[3][e][lane];
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kHWaves; ++w) v += red[w][e][lane];
       const int ii = m0 + 4 * kq + e;
       if (ii < M && j < r) H[(size_t)ii * r + j] = h2f(f2h_rn(v));
     }
@@ -200,7 +206,7 @@ hipError_t launch_lora_h(const uint16_t* X, const uint16_t* A, int M, int K, int
   const int vec = ((reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (reinterpret_cast<uintptr_t>(A) & 15u) == 0 &&
                    (K % 8) == 0) ? 1 : 0;
   const dim3 grid((M + 15) / 16, (r + 15) / 16);
-  hipLaunchKernelGGL(lora_h_kernel, grid, dim3(256), 0, stream, X, A, M, K, r, H, vec);
+  hipLaunchKernelGGL(lora_h_kernel, grid, dim3(64 * kHWaves), 0, stream, X, A, M, K, r, H, vec);
   return hipGetLastError();
 }
 

@@ -324,27 +324,34 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
     if (a.r > 0 && split == 0) {
       // acc += s * H . B^T on the matrix core in fp32 (V_MFMA_F32_16X16X4_F32: A = s*H,
       // lane l holds row l%16, k = l/16; B = B^T, lane l holds k = l/16, column l%16).
-      for (int kr = 0; kr < a.r; kr += 4) {
-        const int k = kr + kq;
-        const int kc = min(k, a.r - 1);
-        float hv[8], bv[4];
+      // 16 ranks per batch: all their H and B loads are issued before the batch's MFMAs, so a
+      // batch costs one load round trip (ranks past r read as zero).
+      for (int kb = 0; kb < a.r; kb += 16) {
+        float hv[4][8], bv[4][4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int ma = m0 + 128 * wm + 16 * i + r;
-          const float h = a.H[(size_t)min(ma, a.M - 1) * a.r + kc];
-          hv[i] = (ma < a.M && k < a.r) ? a.scale * h : 0.f;
+        for (int u = 0; u < 4; ++u) {
+          const int k = kb + 4 * u + kq;
+          const int kc = min(k, a.r - 1);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int ma = m0 + 128 * wm + 16 * i + r;
+            const float h = a.H[(size_t)min(ma, a.M - 1) * a.r + kc];
+            hv[u][i] = (ma < a.M && k < a.r) ? a.scale * h : 0.f;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int n = n0 + 64 * wn + 16 * j + r;
+            const float b = h2f(a.B[(size_t)min(n, a.N - 1) * a.r + kc]);
+            bv[u][j] = (n < a.N && k < a.r) ? b : 0.f;
+          }
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int n = n0 + 64 * wn + 16 * j + r;
-          const float b = h2f(a.B[(size_t)min(n, a.N - 1) * a.r + kc]);
-          bv[j] = (n < a.N && k < a.r) ? b : 0.f;
-        }
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+          for (int i = 0; i < 8; ++i)
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[i], bv[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[u][i], bv[u][j], acc[i][j], 0, 0, 0);
       }
     }
 #pragma unroll
