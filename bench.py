@@ -128,13 +128,13 @@ def op_fn(m, L, x, out):
 
     def fn():
         if M == 1:
-            torch.ops.wlq_fastShot.gemv(m.q_packed_aligned, m.lut_c, x[0], out[0], L.N, L.K, 4, m.chunk_offsets,
-                                        m.chunk_cols, m.chunk_vals, m.lora_B, None, m.dora_gamma, 1.0, 128,
-                                        m.lora_A_f16, m.wlq_prepared)
+            torch.ops.wlq_fastShot.gemv(m.q_packed_aligned, m.lut_c, x[0], out[0], L.N, L.K, L.bits, m.chunk_offsets,
+                                        m.chunk_cols, m.chunk_vals, m.lora_B, None, m.dora_gamma, L.lora_scale,
+                                        L.group_size, m.lora_A_f16, m.wlq_prepared)
         else:
-            torch.ops.wlq_fastShot.gemm(x, m.q_packed_aligned, m.lut_c, out, L.N, L.K, 4, L.wpr, m.chunk_offsets,
-                                        m.chunk_cols, m.chunk_vals, None, m.lora_B, m.dora_gamma, 1.0, 128,
-                                        m.lora_A_f16, m.wlq_prepared)
+            torch.ops.wlq_fastShot.gemm(x, m.q_packed_aligned, m.lut_c, out, L.N, L.K, L.bits, L.wpr, m.chunk_offsets,
+                                        m.chunk_cols, m.chunk_vals, None, m.lora_B, m.dora_gamma, L.lora_scale,
+                                        L.group_size, m.lora_A_f16, m.wlq_prepared)
     return fn
 
 
@@ -222,6 +222,7 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true", help="skip M in {4, 8, 16, 32} per shape (config 1)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="skip the M=2048 GEMM leg")
+    ap.add_argument("--no-cfg3", action="store_true", help="skip the config-3 stress sweep (gate_proj)")
     ap.add_argument("--op", default=None,
                     help="only repeat this product (e.g. gate_up_proj) or 'copy' (256 MiB device copy), for profiling")
     ap.add_argument("--M", type=int, default=1)
@@ -337,6 +338,39 @@ def main() -> int:
         gemm = {"M": M, "TFLOP/s": round(tf, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
                 "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "per_shape": rows}
 
+    # ---- config 3: outlier / adapter stress on gate_proj at M = 1 and M = 512, one factor at a time
+    # around the base case (d = 0.5%, r = 16, G = 128, 4-bit); 20% of rows are heavy (10x the
+    # light rows' outliers) in every case.  3-bit layers have no prepared layout (row-aligned kernel).
+    cfg3 = None
+    if not args.no_cfg3:
+        from qwen_wlqfastshot_helen_beta_amd import synth
+
+        base = {"bits": 4, "group_size": 128, "rank": 16, "density": 0.005}
+        cases = [("d0.1%", {"density": 0.001}), ("d0.5%", {}), ("d1%", {"density": 0.01}), ("d2%", {"density": 0.02}),
+                 ("r0", {"rank": 0}), ("r8", {"rank": 8}), ("r64", {"rank": 64}), ("G64", {"group_size": 64}),
+                 ("3bit", {"bits": 3})]
+        rows3 = {}
+        for cname, over in cases:
+            kw = dict(base)
+            kw.update(over)
+            L = synth.make_layer(*synth.QWEN25_7B_SHAPES["gate_proj"], seed=30, heavy_frac=0.2, heavy_mult=10, **kw)
+            row = dict(kw)
+            for M in (1, 512):
+                ms = op_time(L, M, reps=5)
+                if M == 1:
+                    gbs = L.headline_bytes() / (ms * 1e-3) / 1e9
+                    row["M1"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                else:
+                    tf = 2.0 * M * L.N * L.K / (ms * 1e-3) / 1e12
+                    row["M512"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                                   "frac_mfma": round(tf / MFMA_FP16_PEAK_TFLOPS, 4)}
+            row["nnz"] = int(L.nnz)
+            rows3[cname] = row
+            log(f"[bench] cfg3 {cname:6s}: M=1 {row['M1']['us']:7.2f} us ({row['M1']['GB/s']:6.0f} GB/s), "
+                f"M=512 {row['M512']['us']:7.1f} us ({row['M512']['TFLOP/s']:6.1f} TFLOP/s)")
+            del L
+        cfg3 = {"shape": "gate_proj 18944x3584", "heavy_rows": "20% of rows at 10x", "cases": rows3}
+
     # ---- what this box sustains on plain work: a dense fp16 GEMM through torch (hipBLASLt)
     # at the gate shape and M = 2048, and a device-to-device copy of 512 MiB
     box = box_peaks(dev) if not args.no_gemm else None
@@ -381,6 +415,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "gemm_m2048": gemm,
         "gemm_m128": gemm128,
+        "cfg3": cfg3,
         "box_peaks": box,
         "per_shape": per_shape,
     }
