@@ -57,8 +57,8 @@ namespace {
 #ifndef WLQ_STREAM_BLOCKS_PER_CU
 #define WLQ_STREAM_BLOCKS_PER_CU 4
 #endif
-#ifndef WLQ_STREAM_BLOCKS_PER_CU_M2
-#define WLQ_STREAM_BLOCKS_PER_CU_M2 1  // M <= 2 (one tile per block): fewer K splits, fewer partial round trips
+#ifndef WLQ_STREAM_CUS_PER_BLOCK_M2
+#define WLQ_STREAM_CUS_PER_BLOCK_M2 2  // M <= 2 (one tile per block): split K only below CUs / 2 tile blocks
 #endif
 #ifndef WLQ_STREAM_WAVES_PER_EU
 #define WLQ_STREAM_WAVES_PER_EU 5
@@ -750,7 +750,9 @@ StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank) {
   const int nch = (K + 511) / 512;
   p.tpb = M <= 2 ? 1 : 4;
   const int TB = (T + p.tpb - 1) / p.tpb;
-  const int target = (M <= 2 ? WLQ_STREAM_BLOCKS_PER_CU_M2 : kBlocksPerCU) * std::max(1, cu_count);
+  // M <= 2: a K split costs a partial round trip that outweighs the parallelism it adds unless the
+  // layer has very few tiles; larger M: ~4 blocks per CU.
+  const int target = M <= 2 ? std::max(1, cu_count / WLQ_STREAM_CUS_PER_BLOCK_M2) : kBlocksPerCU * std::max(1, cu_count);
   int splits = std::max(1, std::min(nch, (target + TB - 1) / TB));
   int cps = (nch + splits - 1) / splits;
   const int cps_max = std::max(1, kXBudget / (M * 1024));
