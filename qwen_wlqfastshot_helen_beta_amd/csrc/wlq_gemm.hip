@@ -28,9 +28,10 @@
 //
 // The producer loop runs one 512-column outlier chunk (640 for 3-bit) per trip
 // with its steps unrolled, so everything tied to chunk boundaries is fixed at
-// compile time.  Outlier entries of the block's 128 rows are prepared per
-// (N tile, chunk) by tile_entries_kernel (row prefix + entries in row order),
-// staged into LDS one chunk ahead, and each W thread walks its row's entries.
+// compile time.  Outliers are prepared per (N tile, chunk) and producer thread by
+// tile_entries_kernel: a column mask per step and the values in column order; a W
+// thread holds its record in registers (loaded a chunk ahead) and writes the values
+// of a step's set bits over its dequantized columns.
 //
 // DoRA: the low-rank term s * H . B^T is added in the epilogue of split 0 with
 // V_MFMA_F32_16X16X4_F32 (fp32 operands, exact products) and every split scales
@@ -53,9 +54,14 @@ constexpr int BN = 128;
 constexpr int BK = 64;
 constexpr int NT = 512;
 constexpr int NP = 256;          // producer threads (waves 4..7)
-constexpr int kEntCap = 2048;    // outlier entries of one (N tile, chunk) held in LDS
-constexpr int kPosWords = 132;   // row prefix (BN + 1 used), padded to 16 bytes
-constexpr int kSlotWords = kPosWords + kEntCap;  // one (N tile, chunk) slot of the prepared entries
+// Outlier records, one slot of kOlSlot words per (N tile, chunk); producer thread t handles row
+// t / 2 of the tile, columns 32 (t % 2) + [0, 32) of each 64-column K step:
+//   [kOlSteps][NP] masks: bit c of mask[s][t] = an outlier at that column of step s
+//   [NP]           counts: the thread's entries in the chunk
+//   [NP][4]        up to kOlVals e5m2 values per thread, in (step, column) order
+constexpr int kOlSteps = 10;     // K steps per outlier chunk: 640 / 64 (3-bit), 512 / 64 otherwise
+constexpr int kOlVals = 16;
+constexpr int kOlSlot = (kOlSteps + 1) * NP + 4 * NP;
 constexpr int kMaxSplits = 32;
 constexpr int kXcds = 8;
 
@@ -78,14 +84,12 @@ struct GemmArgs {
   int ksteps_per_split, splits;
   int tiles_m, tiles_n, tiles;
   int has_csr;
-  const uint32_t* tent;  // prepared entries [tiles_n * nch] slots, or nullptr (direct CSR reads)
+  const uint32_t* tent;  // outlier records [tiles_n * nch][kOlSlot], or nullptr (direct CSR reads)
 };
 
 struct GemmSmem {
   uint16_t a[2][BM * BK];
   uint16_t b[2][BN * BK];
-  uint32_t ent[2][kEntCap];   // col | val << 16, the tile's rows in order
-  int pos[2][kPosWords];      // row start inside ent (exclusive prefix), pos[BN] = total
 };
 
 __device__ __forceinline__ int group_of(int col, uint32_t magic) { return (int)__umulhi((uint32_t)col, magic); }
@@ -245,24 +249,9 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   const int ck_end = (kt_end + SPC - 1) / SPC;
   const bool has_work = kt_begin < kt_end;
 
-  // Prepared outlier lists are used when every chunk of this block's range fits its
-  // slot; otherwise the producers read the CSR arrays directly (a separate loop, so
-  // the hot loop carries no data-dependent loads).
-  __shared__ int s_direct;
-  bool prepared = false;
-  if constexpr (HAS_CSR) {
-    if (a.tent != nullptr) {
-      if (tid == 0) s_direct = 0;
-      __syncthreads();
-      if (tid < ck_end - ck_begin &&
-          (int)a.tent[((size_t)tn * a.nch + ck_begin + tid) * kSlotWords + BN] > kEntCap)
-        s_direct = 1;
-      __syncthreads();
-      prepared = s_direct == 0;
-    }
-  }
-  // barriers of the prologue: staging, plus the entries of the first chunk when prepared
-  const int prologue_barriers = (HAS_CSR && prepared) ? 2 : 1;
+  // Outlier records (when the workspace holds them) or direct reads of the CSR arrays.
+  const bool prepared = HAS_CSR && a.tent != nullptr;
+  const int prologue_barriers = 1;
 
   if (wave < 4) {
     // ------------------------------------------------------------ consumer waves
@@ -412,6 +401,26 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   }
   LutPlanes<BITS> pl_pair;  // kLutPair: planes of the current two-step group
 
+  // Outliers.  Prepared: at the start of the step that stages step st of chunk ck (before that
+  // step's prefetch loads, so waiting for them leaves the prefetch in flight) the thread loads
+  // its column mask of that step and, for a chunk's first step, its count and values (up to
+  // kOlVals, in (step, column) order).  A step costs one test when its mask is empty; each set
+  // bit writes the next value.  A thread with more than kOlVals entries in a chunk, or no records
+  // at all, reads the row's CSR entries of the chunk directly.
+  uint32_t om = 0u, oc = 0u;
+  u32x4_t ov = {0u, 0u, 0u, 0u};
+  int orank = 0;
+  auto ol_issue = [&](int ck, auto st_c) __attribute__((always_inline)) {
+    constexpr int ST = decltype(st_c)::value;
+    const uint32_t* slot = a.tent + ((size_t)tn * a.nch + ck) * kOlSlot;
+    om = slot[ST * NP + ptid];
+    if constexpr (ST == 0) {
+      oc = slot[kOlSteps * NP + ptid];
+      ov = reinterpret_cast<const u32x4_t*>(slot + (kOlSteps + 1) * NP)[ptid];
+      orank = 0;
+    }
+  };
+
   // Loads of step kt into S.  EVEN: the step's index from the range start is even.
   auto load_step = [&](StepRegs<BITS>& S, int kt, auto even_c) __attribute__((always_inline)) {
     constexpr bool kEven = decltype(even_c)::value;
@@ -476,71 +485,41 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
     });
   };
 
-  // running position in the row's staged entries (entries are sorted by column)
-  // Walk over the row's staged entries (sorted by column): p_run indexes the entry in
-  // e0, e1 holds the one after (entries past the row's end read as column 0xFFFF), so
-  // a step's test needs no LDS round trip; an entry taken is refilled two ahead.
-  int p_run = 0, p_end = 0;
-  uint32_t e0 = ~0u, e1 = ~0u;
-
-  // Outliers of step (chunk ck, KIN columns into it) overwritten into the W tile in buf.
-  auto store_outliers = [&](int ck, int buf, auto kin_c, auto prep) __attribute__((always_inline)) {
-    constexpr int KIN = decltype(kin_c)::value;
-    constexpr bool kPrep = decltype(prep)::value;
-    const int cb = ck & 1;
-    const int lo = KIN + 32 * hh;  // my 32 columns inside the chunk
-    uint16_t* brow = &sm.b[buf][nl * BK];
-    if (brow_ok) {
-      if constexpr (kPrep) {
-        const uint32_t* ent = sm.ent[cb];
-        if constexpr (KIN == 0) {
-          p_run = sm.pos[cb][nl];
-          p_end = sm.pos[cb][nl + 1];
-          const uint32_t v0 = ent[min(p_run, kEntCap - 1)], v1 = ent[min(p_run + 1, kEntCap - 1)];
-          e0 = p_run < p_end ? v0 : ~0u;
-          e1 = p_run + 1 < p_end ? v1 : ~0u;
-        }
-        while ((int)(e0 & 0xFFFFu) < lo + 32) {
-          const int col = (int)(e0 & 0xFFFFu);
-          if (col >= lo) {
-            const int cs = col - lo;  // column inside my 32
-            brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + (cs & 7)] = (uint16_t)((e0 >> 16) << 8);
-          }
-          ++p_run;
-          const uint32_t v = ent[min(p_run + 1, kEntCap - 1)];
-          e0 = e1;
-          e1 = p_run + 1 < p_end ? v : ~0u;
-        }
-      } else {  // no prepared list (or a chunk beyond its capacity): read the row's chunk directly
-        const int32_t* offr = a.offsets + (size_t)nb * (a.nch + 1);
-        const int s1 = offr[ck + 1];
-        for (int e = offr[ck]; e < s1; ++e) {
-          const int col = (int)a.cols[e];
-          if (col >= lo && col < lo + 32) {
-            const int cs = col - lo;
-            brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + (cs & 7)] = (uint16_t)((uint32_t)a.vals[e] << 8);
-          }
-        }
+  auto direct_walk = [&](int ck, int lo, uint16_t* brow) __attribute__((always_inline)) {
+    const int32_t* offr = a.offsets + (size_t)nb * (a.nch + 1);
+    const int s1 = offr[ck + 1];
+    for (int e = offr[ck]; e < s1; ++e) {
+      const int col = (int)a.cols[e];
+      if (col >= lo && col < lo + 32 && ck * a.chunk + col < a.K) {
+        const int cs = col - lo;
+        brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + (cs & 7)] = (uint16_t)((uint32_t)a.vals[e] << 8);
       }
     }
   };
 
-  // Prepared outlier entries of a chunk (slot of this N tile): loaded into registers
-  // at the first step of the previous chunk, written to ent/pos[ck & 1] two steps
-  // before the chunk's first step is staged (after every reader of that buffer).
-  u32x4_t ent_r[2], pos_r;
-  auto ent_load = [&](int ck) __attribute__((always_inline)) {
-    const uint32_t* slot = a.tent + ((size_t)tn * a.nch + ck) * kSlotWords;
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      ent_r[h] = *reinterpret_cast<const u32x4_t*>(slot + kPosWords + 4 * (ptid + NP * h));
-    pos_r = *reinterpret_cast<const u32x4_t*>(slot + 4 * min(ptid, kPosWords / 4 - 1));
-  };
-  auto ent_store = [&](int ck) __attribute__((always_inline)) {
-    const int cb = ck & 1;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) *reinterpret_cast<u32x4_t*>(&sm.ent[cb][4 * (ptid + NP * h)]) = ent_r[h];
-    if (ptid < kPosWords / 4) *reinterpret_cast<u32x4_t*>(&sm.pos[cb][4 * ptid]) = pos_r;
+  // Outliers of step (chunk ck, KIN columns into it, mask om) overwritten into the W tile in buf.
+  auto store_outliers = [&](int ck, int buf, auto kin_c, auto prep) __attribute__((always_inline)) {
+    constexpr int KIN = decltype(kin_c)::value;
+    constexpr bool kPrep = decltype(prep)::value;
+    const int lo = KIN + 32 * hh;  // my 32 columns inside the chunk
+    uint16_t* brow = &sm.b[buf][nl * BK];
+    if constexpr (kPrep) {
+      if (oc <= (uint32_t)kOlVals) {
+        uint32_t m = om;
+        while (m != 0u) {
+          const int cs = __builtin_ctz(m);  // column inside my 32
+          m &= m - 1u;
+          const uint32_t w = orank < 8 ? (orank < 4 ? ov.x : ov.y) : (orank < 12 ? ov.z : ov.w);
+          const uint32_t v = (w >> (8 * (orank & 3))) & 0xFFu;
+          ++orank;
+          brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + (cs & 7)] = (uint16_t)(v << 8);
+        }
+      } else if (brow_ok) {
+        direct_walk(ck, lo, brow);
+      }
+    } else if (brow_ok) {
+      direct_walk(ck, lo, brow);
+    }
   };
 
   // Register sets: DIST steps of loads in flight (the sets rotate by step index; even
@@ -549,15 +528,11 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   auto run = [&](auto prep) __attribute__((always_inline)) {
     constexpr bool kPrep = decltype(prep)::value;
     StepRegs<BITS> rs[DIST];  // set d holds steps of index d (mod DIST) from the range start
-    if constexpr (HAS_CSR && kPrep) ent_load(ck_begin);
+    if constexpr (HAS_CSR && kPrep) ol_issue(ck_begin, std::integral_constant<int, 0>{});
     static_for<0, DIST>([&](auto d_c) __attribute__((always_inline)) {
       constexpr int d = decltype(d_c)::value;
       load_step(rs[d], kt_begin + d, std::integral_constant<bool, d % 2 == 0>{});
     });
-    if constexpr (HAS_CSR && kPrep) {
-      ent_store(ck_begin);
-      __syncthreads();
-    }
     store_main(rs[0], kt_begin, 0, std::integral_constant<bool, true>{});
     if constexpr (HAS_CSR) store_outliers(ck_begin, 0, std::integral_constant<int, 0>{}, prep);
     // drain the prologue's loads once: the loop then starts from the same wait state as
@@ -574,6 +549,9 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
         constexpr int s = decltype(s_c)::value;
         constexpr int buf = s & 1;
         const int kt = kb + s;
+        if constexpr (HAS_CSR && kPrep)  // outlier record of the step staged below
+          if (s + 1 < SPC || c + 1 < ck_end)
+            ol_issue(s + 1 < SPC ? c : c + 1, std::integral_constant<int, (s + 1) % SPC>{});
         load_step(rs[s % DIST], kt + DIST, std::integral_constant<bool, s % 2 == 0>{});
         // keep the loads ahead of the stores of the other sets
         __builtin_amdgcn_sched_barrier(0);
@@ -582,10 +560,6 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
           constexpr int KIN = ((s + 1) % SPC) * BK;
           if (s + 1 < SPC || c + 1 < ck_end)
             store_outliers(s + 1 < SPC ? c : c + 1, buf ^ 1, std::integral_constant<int, KIN>{}, prep);
-          if constexpr (kPrep) {
-            if constexpr (s == 0) ent_load(min(c + 1, ck_end - 1));
-            if constexpr (s == SPC - 2) ent_store(c + 1);
-          }
         }
         __syncthreads();
       });
@@ -597,45 +571,63 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
     run(std::integral_constant<bool, false>{});
 }
 
-// Prepared outlier entries: one slot per (N tile, chunk) with the row prefix of the
-// tile's 128 rows and their entries (col | val << 16) in row order; a slot whose
-// entries exceed kEntCap keeps only the prefix (the GEMM then reads that chunk's
-// entries from the CSR arrays directly).
-__global__ __launch_bounds__(BN) void tile_entries_kernel(const int32_t* __restrict__ offsets,
+// Outlier records: one block per (N tile, chunk), one thread per GEMM producer thread (row
+// ptid / 2 of the tile, columns 32 (ptid % 2) + [0, 32) of each 64-column step).  The thread walks
+// its row's entries of the chunk, sets the mask bit of each one in its half (dropping chunk
+// columns past the chunk and global columns past K, as the reference's dequant does) and stores
+// its value at its rank among the set bits, so the values come out in (step, column) order
+// whatever the entry order; a later duplicate of a column overwrites the earlier one.
+__global__ __launch_bounds__(NP) void tile_entries_kernel(const int32_t* __restrict__ offsets,
                                                           const uint16_t* __restrict__ cols,
-                                                          const uint8_t* __restrict__ vals, int N, int nch,
-                                                          uint32_t* __restrict__ tent) {
-  __shared__ int part[BN / 64];
+                                                          const uint8_t* __restrict__ vals, int N, int K, int nch,
+                                                          int chunk, uint32_t* __restrict__ tent) {
   const int tn = blockIdx.x / nch;
   const int ck = blockIdx.x - tn * nch;
   const int t = threadIdx.x;
-  const int n = tn * BN + t;
+  const int n = tn * BN + (t >> 1);
+  const int hh = t & 1;
+  uint32_t mask[kOlSteps];
+#pragma unroll
+  for (int s = 0; s < kOlSteps; ++s) mask[s] = 0u;
   int o1 = 0, o2 = 0;
   if (n < N) {
     o1 = offsets[(size_t)n * (nch + 1) + ck];
     o2 = offsets[(size_t)n * (nch + 1) + ck + 1];
   }
-  const int cnt = o2 - o1;
-  int incl = cnt;  // inclusive prefix inside the wave, then across the waves
+  auto in_half = [&](int c) { return c < chunk && ck * chunk + c < K && ((c >> 5) & 1) == hh; };
+  for (int e = o1; e < o2; ++e) {
+    const int c = (int)cols[e];
+    if (in_half(c)) {
+      const uint32_t bit = 1u << (c & 31);
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int u = __shfl_up(incl, d);
-    if ((t & 63) >= d) incl += u;
+      for (int s = 0; s < kOlSteps; ++s)
+        if ((c >> 6) == s) mask[s] |= bit;
+    }
   }
-  if ((t & 63) == 63) part[t >> 6] = incl;
-  __syncthreads();
-  int total = 0;
+  int cnt = 0;
 #pragma unroll
-  for (int w = 0; w < BN / 64; ++w) {
-    if (w < (t >> 6)) incl += part[w];
-    total += part[w];
+  for (int s = 0; s < kOlSteps; ++s) cnt += __popc(mask[s]);
+  uint32_t* slot = tent + (size_t)blockIdx.x * kOlSlot;
+  uint8_t* rv = reinterpret_cast<uint8_t*>(slot + (kOlSteps + 1) * NP + 4 * t);
+  if (cnt <= kOlVals) {
+    for (int e = o1; e < o2; ++e) {
+      const int c = (int)cols[e];
+      if (in_half(c)) {
+        const int s = c >> 6;
+        const int b = c & 31;
+        int rank = 0;  // bits of the steps before s, then of step s below b
+#pragma unroll
+        for (int q = 0; q < kOlSteps; ++q) {
+          if (q < s) rank += __popc(mask[q]);
+          if (q == s) rank += __popc(mask[q] & ((1u << b) - 1u));
+        }
+        rv[rank] = vals[e];
+      }
+    }
   }
-  uint32_t* slot = tent + (size_t)blockIdx.x * kSlotWords;
-  slot[t] = (uint32_t)(incl - cnt);
-  if (t < kPosWords - BN) slot[BN + t] = (uint32_t)total;
-  if (total <= kEntCap)
-    for (int j = 0; j < cnt; ++j)
-      slot[kPosWords + incl - cnt + j] = (uint32_t)cols[o1 + j] | ((uint32_t)vals[o1 + j] << 16);
+#pragma unroll
+  for (int s = 0; s < kOlSteps; ++s) slot[s * NP + t] = mask[s];
+  slot[kOlSteps * NP + t] = (uint32_t)cnt;
 }
 
 template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC>
@@ -696,7 +688,7 @@ SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes)
   const int target = std::max(1, cu_count);  // one 512-thread block per CU (LDS-bound)
   // prepared outlier entries, when the workspace holds them
   const size_t ent_bytes = (L.offsets != nullptr)
-                               ? (size_t)((L.N + BN - 1) / BN) * (size_t)L.nch * kSlotWords * sizeof(uint32_t)
+                               ? (size_t)((L.N + BN - 1) / BN) * (size_t)L.nch * kOlSlot * sizeof(uint32_t)
                                : 0;
   const size_t ent_room = workspace_bytes >= ent_bytes ? ent_bytes : 0;
   int splits = 1;
@@ -759,8 +751,8 @@ hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_
   a.tent = nullptr;
   if (a.has_csr && plan.aux_bytes > 0) {
     a.tent = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(workspace) + part_bytes);
-    hipLaunchKernelGGL(tile_entries_kernel, dim3(a.tiles_n * L.nch), dim3(BN), 0, stream, L.offsets, L.cols,
-                       L.vals, L.N, L.nch, const_cast<uint32_t*>(a.tent));
+    hipLaunchKernelGGL(tile_entries_kernel, dim3(a.tiles_n * L.nch), dim3(NP), 0, stream, L.offsets, L.cols,
+                       L.vals, L.N, L.K, L.nch, L.chunk, const_cast<uint32_t*>(a.tent));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
