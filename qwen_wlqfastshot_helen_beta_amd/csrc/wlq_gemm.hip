@@ -54,14 +54,14 @@ constexpr int BN = 128;
 constexpr int BK = 64;
 constexpr int NT = 512;
 constexpr int NP = 256;          // producer threads (waves 4..7)
-// Outlier records, one slot of kOlSlot words per (N tile, chunk); producer thread t handles row
-// t / 2 of the tile, columns 32 (t % 2) + [0, 32) of each 64-column K step:
-//   [kOlSteps][NP] masks: bit c of mask[s][t] = an outlier at that column of step s
-//   [NP]           counts: the thread's entries in the chunk
-//   [NP][4]        up to kOlVals e5m2 values per thread, in (step, column) order
+// Outlier records, one slot of ol_slot_words(spc) words per (N tile, chunk), spc = K steps per
+// chunk; producer thread t handles row t / 2 of the tile, columns 32 (t % 2) + [0, 32) of each
+// 64-column K step:
+//   [spc][NP]    masks: bit c of mask[s][t] = an outlier at that column of step s
+//   [spc][NP][2] the first kOlVals e5m2 values of (s, t) in column order
 constexpr int kOlSteps = 10;     // K steps per outlier chunk: 640 / 64 (3-bit), 512 / 64 otherwise
-constexpr int kOlVals = 16;
-constexpr int kOlSlot = (kOlSteps + 1) * NP + 4 * NP;
+constexpr int kOlVals = 8;
+constexpr int ol_slot_words(int spc) { return 3 * spc * NP; }
 constexpr int kMaxSplits = 32;
 constexpr int kXcds = 8;
 
@@ -84,7 +84,7 @@ struct GemmArgs {
   int ksteps_per_split, splits;
   int tiles_m, tiles_n, tiles;
   int has_csr;
-  const uint32_t* tent;  // outlier records [tiles_n * nch][kOlSlot], or nullptr (direct CSR reads)
+  const uint32_t* tent;  // outlier records [tiles_n * nch][ol_slot_words], or nullptr (direct CSR reads)
 };
 
 struct GemmSmem {
@@ -403,22 +403,18 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
 
   // Outliers.  Prepared: at the start of the step that stages step st of chunk ck (before that
   // step's prefetch loads, so waiting for them leaves the prefetch in flight) the thread loads
-  // its column mask of that step and, for a chunk's first step, its count and values (up to
-  // kOlVals, in (step, column) order).  A step costs one test when its mask is empty; each set
-  // bit writes the next value.  A thread with more than kOlVals entries in a chunk, or no records
-  // at all, reads the row's CSR entries of the chunk directly.
-  uint32_t om = 0u, oc = 0u;
-  u32x4_t ov = {0u, 0u, 0u, 0u};
-  int orank = 0;
+  // its column mask of that step and the step's first kOlVals values.  A step costs one test when
+  // its mask is empty; each set bit writes the next value.  A step with more than kOlVals
+  // outliers in the thread's 32 columns, or no records at all, reads the row's CSR entries of the
+  // chunk directly for that step.
+  uint32_t om = 0u, ov0 = 0u, ov1 = 0u;
   auto ol_issue = [&](int ck, auto st_c) __attribute__((always_inline)) {
     constexpr int ST = decltype(st_c)::value;
-    const uint32_t* slot = a.tent + ((size_t)tn * a.nch + ck) * kOlSlot;
+    const uint32_t* slot = a.tent + ((size_t)tn * a.nch + ck) * ol_slot_words(SPC);
     om = slot[ST * NP + ptid];
-    if constexpr (ST == 0) {
-      oc = slot[kOlSteps * NP + ptid];
-      ov = reinterpret_cast<const u32x4_t*>(slot + (kOlSteps + 1) * NP)[ptid];
-      orank = 0;
-    }
+    const uint32_t* vw = slot + SPC * NP + 2 * (ST * NP + ptid);
+    ov0 = vw[0];
+    ov1 = vw[1];
   };
 
   // Loads of step kt into S.  EVEN: the step's index from the range start is even.
@@ -504,14 +500,14 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
     const int lo = KIN + 32 * hh;  // my 32 columns inside the chunk
     uint16_t* brow = &sm.b[buf][nl * BK];
     if constexpr (kPrep) {
-      if (oc <= (uint32_t)kOlVals) {
+      if (__popc(om) <= kOlVals) {
         uint32_t m = om;
+        int rank = 0;
         while (m != 0u) {
           const int cs = __builtin_ctz(m);  // column inside my 32
           m &= m - 1u;
-          const uint32_t w = orank < 8 ? (orank < 4 ? ov.x : ov.y) : (orank < 12 ? ov.z : ov.w);
-          const uint32_t v = (w >> (8 * (orank & 3))) & 0xFFu;
-          ++orank;
+          const uint32_t v = ((rank < 4 ? ov0 : ov1) >> (8 * (rank & 3))) & 0xFFu;
+          ++rank;
           brow[8 * ((4 * hh + (cs >> 3)) ^ wsw) + (cs & 7)] = (uint16_t)(v << 8);
         }
       } else if (brow_ok) {
@@ -604,30 +600,25 @@ __global__ __launch_bounds__(NP) void tile_entries_kernel(const int32_t* __restr
         if ((c >> 6) == s) mask[s] |= bit;
     }
   }
-  int cnt = 0;
+  const int spc = chunk / BK;
+  uint32_t* slot = tent + (size_t)blockIdx.x * ol_slot_words(spc);
+  uint8_t* rv = reinterpret_cast<uint8_t*>(slot + spc * NP);  // [spc][NP][8] bytes
+  for (int e = o1; e < o2; ++e) {
+    const int c = (int)cols[e];
+    if (in_half(c)) {
+      const int s = c >> 6;
+      const int b = c & 31;
+      uint32_t ms = 0u;
 #pragma unroll
-  for (int s = 0; s < kOlSteps; ++s) cnt += __popc(mask[s]);
-  uint32_t* slot = tent + (size_t)blockIdx.x * kOlSlot;
-  uint8_t* rv = reinterpret_cast<uint8_t*>(slot + (kOlSteps + 1) * NP + 4 * t);
-  if (cnt <= kOlVals) {
-    for (int e = o1; e < o2; ++e) {
-      const int c = (int)cols[e];
-      if (in_half(c)) {
-        const int s = c >> 6;
-        const int b = c & 31;
-        int rank = 0;  // bits of the steps before s, then of step s below b
-#pragma unroll
-        for (int q = 0; q < kOlSteps; ++q) {
-          if (q < s) rank += __popc(mask[q]);
-          if (q == s) rank += __popc(mask[q] & ((1u << b) - 1u));
-        }
-        rv[rank] = vals[e];
-      }
+      for (int q = 0; q < kOlSteps; ++q)
+        if (q == s) ms = mask[q];
+      const int rank = __popc(ms & ((1u << b) - 1u));  // set bits of the step below b
+      if (rank < kOlVals) rv[((size_t)s * NP + t) * 8 + rank] = vals[e];
     }
   }
 #pragma unroll
-  for (int s = 0; s < kOlSteps; ++s) slot[s * NP + t] = mask[s];
-  slot[kOlSteps * NP + t] = (uint32_t)cnt;
+  for (int s = 0; s < kOlSteps; ++s)
+    if (s < spc) slot[s * NP + t] = mask[s];
 }
 
 template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC>
@@ -688,7 +679,7 @@ SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes)
   const int target = std::max(1, cu_count);  // one 512-thread block per CU (LDS-bound)
   // prepared outlier entries, when the workspace holds them
   const size_t ent_bytes = (L.offsets != nullptr)
-                               ? (size_t)((L.N + BN - 1) / BN) * (size_t)L.nch * kOlSlot * sizeof(uint32_t)
+                               ? (size_t)((L.N + BN - 1) / BN) * (size_t)L.nch * ol_slot_words(spc) * sizeof(uint32_t)
                                : 0;
   const size_t ent_room = workspace_bytes >= ent_bytes ? ent_bytes : 0;
   int splits = 1;
