@@ -105,7 +105,7 @@ int wlq_gemm(const void* X, const int32_t* q_packed, const void* lut_c, void* ou
              float lora_scale, int32_t r, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Bytes of the prepared (tile-contiguous) layout of a layer, or 0 when the
- * layer has none (it needs 4-bit codes, a per-row LUT or a group size that is a
+ * layer has none (it needs 4-bit or 3-bit codes, a per-row LUT or a group size that is a
  * multiple of 32, K % 8 == 0 and K < 65536).  nnz = number of outlier entries.
  * No reference counterpart: the reference streams its row-aligned layout
  * directly (csrc/gemv_kernel.cu:168-190); this layout is built once at load
@@ -115,7 +115,8 @@ size_t wlq_prepared_bytes(int64_t N, int64_t K, int32_t bits, int32_t group_size
 
 /* Device: build the prepared layout from the reference-format tensors into
  * `prepared` (256-byte aligned, wlq_prepared_bytes() bytes): codes in 16-row x
- * 128-column tiles in MFMA lane order, LUT byte planes per 16-row tile, and per
+ * 128-column tiles in MFMA lane order (3-bit codes widened to 4-bit nibbles, their
+ * 8-entry LUTs zero-padded to 16), LUT byte planes per 16-row tile, and per
  * outlier its column and the fp32 delta fp16(e5m2 << 8) - lut[code] of the
  * reference's GEMV outlier correction (csrc/gemv_kernel.cu:262-288). */
 int wlq_prepare(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K, int32_t bits, int32_t group_size,

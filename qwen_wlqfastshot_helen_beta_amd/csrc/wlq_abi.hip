@@ -209,8 +209,9 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
   const wlq::SplitPlan p = skinny ? wlq::plan_skinny(L, (int)M, cus, unlimited, fused ? r : 0)
                                   : wlq::plan_gemm(L, (int)M, cus, unlimited);
   size_t need = hb + p.workspace_bytes;
-  if (M <= wlq::stream_max_m() && bits == 4) {  // the prepared-layout kernel may serve the call
-    const wlq::StreamPlan sp = wlq::plan_stream((int)N, (int)K, (int)M, cus, r > 0 && r <= wlq::stream_max_rank() ? r : 0);
+  if (M <= wlq::stream_max_m() && (bits == 4 || bits == 3)) {  // the prepared-layout kernel may serve the call
+    const wlq::StreamPlan sp = wlq::plan_stream((int)N, (int)K, (int)M, cus,
+                                                r > 0 && r <= wlq::stream_max_rank() ? r : 0, L.chunk);
     need = std::max(need, sp.workspace_bytes + 256);
   }
   return need > 0 ? wlq::kSyncBytes + need : 0;
@@ -235,7 +236,7 @@ int wlq_prepare(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K
     return WLQ_ERR_BAD_SHAPE;
   }
   if (!wlq::prepared_supported(L.N, L.K, L.bits, L.group_size)) {
-    wlq::set_error("wlq_prepare: no prepared layout for bits=%d, group_size=%d, K=%lld (needs 4-bit, a per-row LUT "
+    wlq::set_error("wlq_prepare: no prepared layout for bits=%d, group_size=%d, K=%lld (needs 4- or 3-bit, a per-row LUT "
                    "or a group size multiple of 32, K %% 8 == 0, K < 65536)",
                    (int)bits, (int)group_size, (long long)K);
     return WLQ_ERR_UNSUPPORTED;
@@ -303,7 +304,7 @@ int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c,
     const bool aligned = (reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (reinterpret_cast<uintptr_t>(prepared) & 255u) == 0 &&
                          (!fused_h || (reinterpret_cast<uintptr_t>(D.A) & 15u) == 0) && dora_ok;
     const wlq::StreamPlan p =
-        wlq::plan_stream(L.N, L.K, (int)M, current_cu_count(), fused_h ? D.r : 0);
+        wlq::plan_stream(L.N, L.K, (int)M, current_cu_count(), fused_h ? D.r : 0, L.chunk);
     const bool need_sync = p.splits > 1 || fused_h;
     const size_t ws = workspace != nullptr ? workspace_bytes : 0;
     const bool ws_ok = !need_sync || ws >= wlq::kSyncBytes + p.workspace_bytes;

@@ -61,7 +61,7 @@ hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_
 
 hipError_t launch_dequant(const Layer& L, uint16_t* W, hipStream_t stream);
 
-// Prepared (tile-contiguous) layout of a 4-bit layer for the streaming decode kernel
+// Prepared (tile-contiguous) layout of a 4-bit or 3-bit layer for the streaming decode kernel
 // (wlq_stream.hip): byte offsets of its four parts inside one buffer.
 struct PreparedLayout {
   int T, S, ng;             // row tiles of 16, slabs of 128 columns, LUT groups per row
@@ -80,7 +80,7 @@ struct StreamPlan {
 };
 int stream_max_m();
 int stream_max_rank();
-StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank);
+StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank, int chunk);  // chunk: outlier chunk width
 hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, const Dora& D, const uint16_t* x,
                          uint16_t* out, int M, const StreamPlan& plan, float* workspace, uint32_t* sync,
                          hipStream_t stream);

@@ -1,5 +1,7 @@
 // Decode product on the prepared (tile-contiguous) layout: M = 1..32 activation
-// rows, 4-bit codes, per-row LUTs or LUT groups of a multiple of 32 columns.
+// rows, 4-bit or 3-bit codes (3-bit codes are stored as 4-bit nibbles against
+// their 8-entry LUTs padded to 16), per-row LUTs or LUT groups of a multiple of
+// 32 columns.
 //
 // Reference behaviour replaced: gemv_chunk_csr_kernel + launch_gemv_chunk_csr
 // (csrc/gemv_kernel.cu:86-320, :396-457) and the split-K reduce
@@ -13,7 +15,7 @@
 // Prepared layout (built once per layer by the prepare kernels below, from the
 // reference's row-aligned codes, LUTs and chunk CSR):
 //   codes  u32x4 [T][S][64]     T = ceil(N/16) row tiles, S = ceil(K/128) slabs;
-//                               lane l = r + 16*kq holds the 32 codes of row
+//                               lane l = r + 16*kq holds the 32 nibble codes of row
 //                               16t + r, columns 128s + 32kq .. +31 (4 words), so
 //                               one wave load is 1 KB contiguous and lands in the
 //                               MFMA B-operand lane order.
@@ -96,6 +98,7 @@ struct StreamArgs {
   int M, N, K, S, ng, nch, T, TB;
   uint32_t g_magic;        // floor(c / G) == umulhi(c, g_magic) for c < 2^20
   int splits, cps;         // K splits per tile block, outlier chunks per split
+  int spc;                 // slabs per outlier chunk (4; 5 for 3-bit's 640-column chunks)
   int xstride;             // halves per staged activation row
   int h_blocks;
   float* partial;          // [splits, M, N]
@@ -253,8 +256,8 @@ void stream4_kernel(const StreamArgs a) {
   const int ph = wave % WPT;
   const int c0 = split * a.cps;
   const int c1 = min(a.nch, c0 + a.cps);
-  const int s0 = 4 * c0;
-  const int s1 = min(a.S, 4 * c1);
+  const int s0 = a.spc * c0;
+  const int s1 = min(a.S, a.spc * c1);
   const int nw = (s1 - s0 - ph + WPT - 1) / WPT;  // this wave's slabs (may be 0)
   const int s_last = min(s0 + ph + WPT * max(nw - 1, 0), s1 - 1);  // prefetch clamp (in range)
 
@@ -620,8 +623,10 @@ void stream4_kernel(const StreamArgs a) {
 
 // ---------------------------------------------------------------- preparation
 
-__global__ __launch_bounds__(256) void prep_codes_kernel(const uint32_t* __restrict__ q, int N, int wpr, int T, int S,
-                                                         u32x4_t* __restrict__ codes) {
+// 4-bit rows are copied word for word; 3-bit rows (ten codes per word, bits 3c..3c+2)
+// are rewritten as eight nibble codes per word, columns >= K as code 0.
+__global__ __launch_bounds__(256) void prep_codes_kernel(const uint32_t* __restrict__ q, int N, int K, int wpr,
+                                                         int bits, int T, int S, u32x4_t* __restrict__ codes) {
   const size_t total = (size_t)T * S * 64;
   for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
     const int l = (int)(idx & 63);
@@ -631,13 +636,29 @@ __global__ __launch_bounds__(256) void prep_codes_kernel(const uint32_t* __restr
     const int n = 16 * t + (l & 15);
     const int w0 = 16 * s + 4 * (l >> 4);
     u32x4_t v = {0u, 0u, 0u, 0u};
-    if (n < N && w0 + 4 <= wpr) v = *reinterpret_cast<const u32x4_t*>(q + (size_t)n * wpr + w0);
+    if (bits == 4) {
+      if (n < N && w0 + 4 <= wpr) v = *reinterpret_cast<const u32x4_t*>(q + (size_t)n * wpr + w0);
+    } else if (n < N) {
+      const uint32_t* qrow = q + (size_t)n * wpr;
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t word = 0u;
+        for (int c = 0; c < 8; ++c) {
+          const int col = 8 * (w0 + j) + c;
+          if (col < K) word |= ((qrow[col / 10] >> (3 * (col % 10))) & 7u) << (4 * c);
+        }
+        w[j] = word;
+      }
+      v = u32x4_t{w[0], w[1], w[2], w[3]};
+    }
     codes[idx] = v;
   }
 }
 
-__global__ __launch_bounds__(256) void prep_planes_kernel(const uint16_t* __restrict__ lut, int N, int ng, int T,
-                                                          u32x4_t* __restrict__ planes) {
+// nl = LUT entries per (row, group): 16, or 8 for 3-bit (entries 8..15 of the planes stay 0).
+__global__ __launch_bounds__(256) void prep_planes_kernel(const uint16_t* __restrict__ lut, int N, int ng, int nl,
+                                                          int T, u32x4_t* __restrict__ planes) {
   const size_t total = (size_t)T * ng * 32;
   for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
     const int rr = (int)(idx & 15);
@@ -648,10 +669,11 @@ __global__ __launch_bounds__(256) void prep_planes_kernel(const uint16_t* __rest
     const int n = 16 * t + rr;
     uint32_t w[4] = {0u, 0u, 0u, 0u};
     if (n < N) {
-      const uint16_t* e = lut + ((size_t)n * ng + g) * 16;
+      const uint16_t* e = lut + ((size_t)n * ng + g) * nl;
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
-        const uint32_t b = p ? (uint32_t)(e[k] >> 8) : (uint32_t)(e[k] & 0xFFu);
+        const uint32_t v = k < nl ? (uint32_t)e[k] : 0u;
+        const uint32_t b = p ? (v >> 8) : (v & 0xFFu);
         w[k >> 2] |= b << (8 * (k & 3));
       }
     }
@@ -665,7 +687,8 @@ __global__ __launch_bounds__(256) void prep_outliers_kernel(const uint32_t* __re
                                                             const int32_t* __restrict__ offsets,
                                                             const uint16_t* __restrict__ cols,
                                                             const uint8_t* __restrict__ vals, int N, int K, int wpr,
-                                                            int ng, int G, int nch, uint16_t* __restrict__ gcol,
+                                                            int bits, int ng, int G, int nch, int chunk,
+                                                            uint16_t* __restrict__ gcol,
                                                             float* __restrict__ delta) {
   const size_t total = (size_t)N * nch;
   for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
@@ -677,15 +700,16 @@ __global__ __launch_bounds__(256) void prep_outliers_kernel(const uint32_t* __re
     const uint32_t* qrow = q + (size_t)n * wpr;
     for (int e = e_lo; e < e_hi; ++e) {
       const int cl = (int)cols[e];
-      const int col = c * 512 + cl;
-      if (cl < 512 && col < K) {
-        const uint32_t code = (qrow[col >> 3] >> (4 * (col & 7))) & 15u;
+      const int col = c * chunk + cl;
+      if (cl < chunk && col < K) {
+        const uint32_t code = bits == 4 ? (qrow[col >> 3] >> (4 * (col & 7))) & 15u
+                                        : (qrow[col / 10] >> (3 * (col % 10))) & 7u;
         const int g = G > 0 ? min(col / G, ng - 1) : 0;
         const float w_true = h2f((uint16_t)((uint32_t)vals[e] << 8));
         gcol[e] = (uint16_t)col;
-        delta[e] = w_true - h2f(lut[((size_t)n * ng + g) * 16 + code]);
-      } else {  // dropped (the reference drops col >= K; a chunk column >= 512 is malformed)
-        gcol[e] = (uint16_t)(c * 512);
+        delta[e] = w_true - h2f(lut[(((size_t)n * ng + g) << bits) + code]);
+      } else {  // dropped (the reference drops col >= K; a chunk column >= the chunk width is malformed)
+        gcol[e] = (uint16_t)(c * chunk);
         delta[e] = 0.f;
       }
     }
@@ -705,8 +729,9 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // ------------------------------------------------------------------ host side
 
 bool prepared_supported(int N, int K, int bits, int group_size) {
-  if (bits != 4 || N <= 0 || K <= 0 || K % 8 != 0 || K > 65535) return false;
-  return group_size == 0 || group_size % 32 == 0;
+  if ((bits != 4 && bits != 3) || N <= 0 || K <= 0 || K % 8 != 0 || K > 65535) return false;
+  // a group covers whole 32-column lane segments and at least one 3-bit code window (40 columns)
+  return group_size == 0 || (group_size % 32 == 0 && group_size >= (bits == 3 ? 40 : 32));
 }
 
 PreparedLayout prepared_layout(int N, int K, int group_size, int64_t nnz) {
@@ -727,27 +752,27 @@ hipError_t launch_prepare(const Layer& L, int64_t nnz, void* prepared, hipStream
   char* base = reinterpret_cast<char*>(prepared);
   auto grid_for = [](size_t total) { return dim3((unsigned)std::min<size_t>((total + 255) / 256, 65535)); };
   const int ng = L.group_size > 0 ? L.ng : 1;
-  hipLaunchKernelGGL(prep_codes_kernel, grid_for((size_t)p.T * p.S * 64), dim3(256), 0, stream, L.q, L.N, L.wpr, p.T,
-                     p.S, reinterpret_cast<u32x4_t*>(base + p.codes_off));
+  hipLaunchKernelGGL(prep_codes_kernel, grid_for((size_t)p.T * p.S * 64), dim3(256), 0, stream, L.q, L.N, L.K, L.wpr,
+                     L.bits, p.T, p.S, reinterpret_cast<u32x4_t*>(base + p.codes_off));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(prep_planes_kernel, grid_for((size_t)p.T * ng * 32), dim3(256), 0, stream, L.lut, L.N, ng, p.T,
-                     reinterpret_cast<u32x4_t*>(base + p.planes_off));
+  hipLaunchKernelGGL(prep_planes_kernel, grid_for((size_t)p.T * ng * 32), dim3(256), 0, stream, L.lut, L.N, ng,
+                     1 << L.bits, p.T, reinterpret_cast<u32x4_t*>(base + p.planes_off));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (L.offsets != nullptr && nnz > 0) {
     hipLaunchKernelGGL(prep_outliers_kernel, grid_for((size_t)L.N * L.nch), dim3(256), 0, stream, L.q, L.lut,
-                       L.offsets, L.cols, L.vals, L.N, L.K, L.wpr, ng, L.group_size, L.nch,
+                       L.offsets, L.cols, L.vals, L.N, L.K, L.wpr, L.bits, ng, L.group_size, L.nch, L.chunk,
                        reinterpret_cast<uint16_t*>(base + p.gcol_off), reinterpret_cast<float*>(base + p.delta_off));
     e = hipGetLastError();
   }
   return e;
 }
 
-StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank) {
+StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank, int chunk) {
   StreamPlan p{};
   const int T = (N + 15) / 16;
-  const int nch = (K + 511) / 512;
+  const int nch = (K + chunk - 1) / chunk;
   p.tpb = M <= 2 ? 1 : 4;
   const int TB = (T + p.tpb - 1) / p.tpb;
   // M <= 2: a K split costs a partial round trip that outweighs the parallelism it adds unless the
@@ -755,7 +780,7 @@ StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank) {
   const int target = M <= 2 ? std::max(1, cu_count / WLQ_STREAM_CUS_PER_BLOCK_M2) : kBlocksPerCU * std::max(1, cu_count);
   int splits = std::max(1, std::min(nch, (target + TB - 1) / TB));
   int cps = (nch + splits - 1) / splits;
-  const int cps_max = std::max(1, kXBudget / (M * 1024));
+  const int cps_max = std::max(1, kXBudget / (M * chunk * 2));
   cps = std::min(cps, cps_max);
   splits = (nch + cps - 1) / cps;
   p.splits = splits;
@@ -769,8 +794,10 @@ StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank) {
   p.hpart_off = hf;
   p.partial_off = hf + hp;
   p.workspace_bytes = hf + hp + part;
-  p.ok = M >= 1 && M <= stream_max_m() && (splits == 1 || TB <= (int)(kSyncBytes / 4) - kSyncTile) &&
-         fused_rank % 8 == 0 && fused_rank <= kMaxRank;
+  // the block's threads stage the activations with kXR (M > 16: 2 kXR) 16-byte loads each
+  const bool staged = (size_t)M * cps * (chunk / 8) <= (size_t)256 * kXR * (M > 16 ? 2 : 1);
+  p.ok = M >= 1 && M <= stream_max_m() && (chunk == 512 || chunk == 640) && staged &&
+         (splits == 1 || TB <= (int)(kSyncBytes / 4) - kSyncTile) && fused_rank % 8 == 0 && fused_rank <= kMaxRank;
   return p;
 }
 
@@ -802,13 +829,14 @@ hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, cons
   a.K = L.K;
   a.S = lay.S;
   a.ng = lay.ng;
-  a.nch = (L.K + 511) / 512;
+  a.nch = (L.K + L.chunk - 1) / L.chunk;
+  a.spc = L.chunk / 128;
   a.T = lay.T;
   a.TB = plan.TB;
   a.g_magic = L.group_size > 0 ? (uint32_t)((0x100000000ull / (uint64_t)L.group_size) + 1ull) : 0u;
   a.splits = plan.splits;
   a.cps = plan.cps;
-  a.xstride = plan.cps * 512 + 8;
+  a.xstride = plan.cps * L.chunk + 8;
   const bool fused_h = D.r > 0 && D.H == nullptr;
   a.h_blocks = fused_h ? plan.h_blocks : 0;
   char* ws = reinterpret_cast<char*>(workspace);

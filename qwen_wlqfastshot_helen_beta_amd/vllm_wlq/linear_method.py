@@ -473,8 +473,8 @@ def attach_synthetic(layer: torch.nn.Module, synth, device, prepared: bool = Tru
 
 def prepare_layer(layer: torch.nn.Module) -> Optional[torch.Tensor]:
     """The layer's load-time tile-contiguous layout for the decode kernel (None when
-    its format has none: only 4-bit codes with a per-row LUT or a group size that is
-    a multiple of 32).  Built on the device from the reference-format tensors, which
+    its format has none: only 4- and 3-bit codes with a per-row LUT or a group size
+    that is a multiple of 32, K % 8 == 0).  Built on the device from the reference-format tensors, which
     the layer keeps for the other kernels and for dequant_w0."""
     t = _C.prepare_layer(layer.q_packed_aligned, layer.lut_c, layer.N, layer.K, int(layer.quant_bits),
                          int(getattr(layer, "wlq_group_size", 0)), layer.chunk_offsets, layer.chunk_cols,

@@ -100,18 +100,25 @@ def prepared_reference(L: synth.SynthLayer):
     """numpy rebuild of the prepared (tile-contiguous) layout from the reference-format
     arrays: (codes u32 [T, S, 64, 4], planes u8 [T, ng, 2, 16, 16], gcol, delta).
     Codes: lane l = r + 16 kq of tile t, slab s holds words 16 s + 4 kq .. +3 of row
-    16 t + r; planes: low / high bytes of the 16 LUT entries of row 16 t + r, group g;
+    16 t + r (4-bit: the row-aligned words as they are; 3-bit: the codes re-packed
+    eight 4-bit nibbles per word, columns >= K zero); planes: low / high bytes of the
+    16 LUT entries of row 16 t + r, group g (3-bit: 8 entries, then zeros);
     gcol / delta: the oracle's outlier_delta."""
     N, K = L.N, L.K
     T, S = -(-N // 16), -(-K // 128)
     ng = 1 if L.group_size <= 0 or L.group_size >= K else -(-K // L.group_size)
-    q = L.q.view(np.uint32).reshape(N, L.wpr)
     qpad = np.zeros((T * 16, S * 16), dtype=np.uint32)
-    qpad[:N, :L.wpr] = q
+    if L.bits == 4:
+        qpad[:N, :L.wpr] = L.q.view(np.uint32).reshape(N, L.wpr)
+    else:
+        c = np.zeros((N, S * 128), dtype=np.uint32)
+        c[:, :K] = O.unpack_row_aligned(L.q, N, K, L.bits)
+        nib = c.reshape(N, S * 16, 8) << (4 * np.arange(8, dtype=np.uint32))
+        qpad[:N] = np.bitwise_or.reduce(nib, axis=2)
     codes = qpad.reshape(T, 16, S, 4, 4).transpose(0, 2, 3, 1, 4).reshape(T, S, 64, 4)
-    lut = L.lut.view(np.uint16).reshape(N, ng, 16)
+    nl = 1 << L.bits
     lpad = np.zeros((T * 16, ng, 16), dtype=np.uint16)
-    lpad[:N] = lut
+    lpad[:N, :, :nl] = L.lut.view(np.uint16).reshape(N, ng, nl)
     planes = np.stack([(lpad & 0xFF).astype(np.uint8), (lpad >> 8).astype(np.uint8)], axis=2)  # [T*16, ng, 2, 16]
     planes = planes.reshape(T, 16, ng, 2, 16).transpose(0, 2, 3, 1, 4)
     gs = 0 if ng == 1 else L.group_size

@@ -19,13 +19,13 @@ def _case(**kw):
     print("[case] " + " ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
 
 
-@pytest.mark.parametrize("gs", [0, 32, 64, 128, 256])
-def test_prepared_layout_bit_exact(vw, gs):
-    for N, K, density in ((77, 1000, 0.02), (64, 512, 0.0), (33, 3584, 0.005)):
-        _case(gs=gs, N=N, K=K, density=density)
-        L = synth.make_layer(N=N, K=K, bits=4, group_size=gs, rank=0, density=density, seed=N + gs)
+@pytest.mark.parametrize("bits,gs", [(4, 0), (4, 32), (4, 64), (4, 128), (4, 256), (3, 0), (3, 64), (3, 128)])
+def test_prepared_layout_bit_exact(vw, bits, gs):
+    for N, K, density in ((77, 1000, 0.02), (64, 512, 0.0), (33, 3584, 0.005), (20, 1928, 0.03)):
+        _case(bits=bits, gs=gs, N=N, K=K, density=density)
+        L = synth.make_layer(N=N, K=K, bits=bits, group_size=gs, rank=0, density=density, seed=N + gs)
         t = L.to_torch(DEV)
-        buf = vw._C.prepare_layer(t["q_packed"], t["lut_c"], N, K, 4, gs, t["chunk_offsets"], t["chunk_cols"],
+        buf = vw._C.prepare_layer(t["q_packed"], t["lut_c"], N, K, bits, gs, t["chunk_offsets"], t["chunk_cols"],
                                   t["chunk_vals"])
         torch.cuda.synchronize()
         assert buf.numel() > 0
@@ -38,8 +38,8 @@ def test_prepared_layout_bit_exact(vw, gs):
 
 
 def test_prepare_unsupported_formats(vw):
-    """3-bit codes and group sizes not a multiple of 32 have no prepared layout."""
-    for bits, gs, K in ((3, 64, 640), (4, 48, 960), (4, 128, 1001)):
+    """2- and 1-bit codes, group sizes not a multiple of 32 and K % 8 != 0 have no prepared layout."""
+    for bits, gs, K in ((2, 64, 640), (1, 128, 1024), (4, 48, 960), (3, 48, 960), (4, 128, 1001)):
         L = synth.make_layer(N=16, K=K, bits=bits, group_size=gs, rank=0, density=0.0, seed=1)
         t = L.to_torch(DEV)
         buf = vw._C.prepare_layer(t["q_packed"], t["lut_c"], L.N, L.K, bits, gs)
@@ -62,6 +62,20 @@ def test_prepared_parity(vw, M):
                 check_close(y, oracle_product(L, x, H, round_gemm_output=None), what=f"M={M} reference rounding")
 
 
+@pytest.mark.parametrize("M", [1, 2, 4, 8, 12, 13, 16, 17, 25, 26, 32])
+def test_prepared_parity_3bit(vw, M):
+    """3-bit layers: codes widened to nibbles, 640-column outlier chunks (5 slabs);
+    M = 13..16 and 26..32 exceed the kernel's activation staging for a 640-column chunk
+    and run the row-aligned kernel instead (same results either way)."""
+    for gs in (0, 64, 128):
+        for dora in ("fused", "h"):
+            _case(M=M, gs=gs, dora=dora, bits=3)
+            L = synth.make_layer(N=200, K=1928, bits=3, group_size=gs, rank=8, density=0.01, seed=300 + M + gs)
+            x = synth.make_activations(M, L.K, seed=M)
+            y, H = run_prepared(vw, L, x, dora=dora)
+            check_close(y, oracle_product(L, x, H), what=f"3-bit M={M} gs={gs} dora={dora}")
+
+
 @pytest.mark.parametrize("shape", [(48, 8192), (16, 3584), (4864, 896), (100, 18944), (512, 3584)])
 def test_prepared_shapes_and_splits(vw, shape):
     """Narrow layers (many K splits), config-0 up_proj, a down_proj-like K."""
@@ -72,6 +86,19 @@ def test_prepared_shapes_and_splits(vw, shape):
         x = synth.make_activations(M, L.K, seed=M + 7)
         y, H = run_prepared(vw, L, x, dora="fused")
         check_close(y, oracle_product(L, x, H), what=f"N={N} K={K} M={M}")
+
+
+@pytest.mark.parametrize("shape", [(48, 8960), (4864, 896), (100, 18944), (3000, 3584)])
+def test_prepared_shapes_3bit(vw, shape):
+    N, K = shape
+    for M in (1, 4, 8):
+        _case(N=N, K=K, M=M, bits=3)
+        L = synth.make_layer(N=N, K=K, bits=3, group_size=64, rank=16, density=0.005, seed=N + K + M)
+        x = synth.make_activations(M, L.K, seed=M + 7)
+        y, H = run_prepared(vw, L, x, dora="fused")
+        check_close(y, oracle_product(L, x, H), what=f"3-bit N={N} K={K} M={M}")
+        b, _ = run_product(vw, L, x, fused_h=True)
+        check_close(y, b.astype(np.float64), tol=1.2e-3, what=f"3-bit prepared vs row layout N={N} K={K} M={M}")
 
 
 def test_prepared_no_outliers_and_heavy_rows(vw):

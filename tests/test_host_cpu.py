@@ -121,7 +121,10 @@ def test_abi_prepared_bytes():
         ng = 1 if G == 0 or G >= K else -(-K // G)
         want = a(T * S * 1024) + a(T * ng * 512) + a(nnz * 2) + a(nnz * 4)
         assert lib.wlq_prepared_bytes(N, K, 4, G, nnz) == want, (N, K, G)
-    assert lib.wlq_prepared_bytes(64, 640, 3, 64, 0) == 0     # 3-bit
+        # 3-bit: the same layout (codes as 4-bit nibbles, LUTs padded to 16); groups of >= 40 columns
+        assert lib.wlq_prepared_bytes(N, K, 3, G, nnz) == (0 if 0 < G < 40 and G < K else want), (N, K, G)
+    assert lib.wlq_prepared_bytes(64, 640, 2, 64, 0) == 0     # 2-bit
+    assert lib.wlq_prepared_bytes(64, 1024, 1, 128, 0) == 0   # 1-bit
     assert lib.wlq_prepared_bytes(64, 960, 4, 48, 0) == 0     # group not a multiple of 32
     assert lib.wlq_prepared_bytes(64, 1001, 4, 128, 0) == 0   # K % 8 != 0
     assert lib.wlq_prepared_bytes(64, 70000, 4, 128, 0) == 0  # columns beyond 16 bits
