@@ -72,7 +72,7 @@ PreparedLayout prepared_layout(int N, int K, int group_size, int64_t nnz);
 hipError_t launch_prepare(const Layer& L, int64_t nnz, void* prepared, hipStream_t stream);
 
 struct StreamPlan {
-  int tpb;                  // row tiles per block (1 or 4)
+  int tpb;                  // row tiles per block (1, 2 or 4)
   int TB, splits, cps;      // tile blocks, K splits, outlier chunks per split
   int h_blocks;             // DoRA blocks when H is computed in the kernel
   size_t hfin_off, hpart_off, partial_off, workspace_bytes;

@@ -773,11 +773,14 @@ StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank, int ch
   StreamPlan p{};
   const int T = (N + 15) / 16;
   const int nch = (K + chunk - 1) / chunk;
-  p.tpb = M <= 2 ? 1 : 4;
-  const int TB = (T + p.tpb - 1) / p.tpb;
   // M <= 2: a K split costs a partial round trip that outweighs the parallelism it adds unless the
   // layer has very few tiles; larger M: ~4 blocks per CU.
   const int target = M <= 2 ? std::max(1, cu_count / WLQ_STREAM_CUS_PER_BLOCK_M2) : kBlocksPerCU * std::max(1, cu_count);
+  // M <= 2: two row tiles per block (14 slabs per wave at K = 3584 instead of 7) halve the
+  // per-block overhead (activation staging, completion) wherever that still leaves target blocks
+  // (gate_up 33.2 -> 29.2 us); larger M: a tile per wave (two per block measured slower there).
+  p.tpb = M > 2 ? 4 : (T / 2 >= target ? 2 : 1);
+  const int TB = (T + p.tpb - 1) / p.tpb;
   int splits = std::max(1, std::min(nch, (target + TB - 1) / TB));
   int cps = (nch + splits - 1) / splits;
   const int cps_max = std::max(1, kXBudget / (M * chunk * 2));
@@ -855,6 +858,10 @@ hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, cons
   const bool per_row = L.group_size <= 0 || lay.ng == 1;
   if (per_row) a.ng = 1;
 #define WLQ_STREAM_DISPATCH(PR)                                                  \
+  if (plan.tpb == 2) {                                                          \
+    if (mb == 1) return launch_tpl<PR, 2, 1>(a, grid, lds, stream);             \
+    return launch_tpl<PR, 2, 2>(a, grid, lds, stream);                          \
+  }                                                                             \
   if (plan.tpb == 1) {                                                          \
     if (mb == 1) return launch_tpl<PR, 1, 1>(a, grid, lds, stream);             \
     return launch_tpl<PR, 1, 2>(a, grid, lds, stream);                          \

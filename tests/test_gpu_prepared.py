@@ -101,6 +101,20 @@ def test_prepared_shapes_3bit(vw, shape):
         check_close(y, b.astype(np.float64), tol=1.2e-3, what=f"3-bit prepared vs row layout N={N} K={K} M={M}")
 
 
+@pytest.mark.parametrize("shape", [(4112, 1024), (4864, 896), (8208, 3584)])
+def test_prepared_two_tiles_per_block(vw, shape):
+    """M <= 2 on layers with >= 256 row tiles: blocks of two 16-row tiles (an odd tile count
+    leaves the last block's second tile past N)."""
+    N, K = shape
+    for M in (1, 2):
+        for gs, dora in ((128, "fused"), (0, "h"), (64, "none")):
+            _case(N=N, K=K, M=M, gs=gs, dora=dora)
+            L = synth.make_layer(N=N, K=K, bits=4, group_size=gs, rank=16, density=0.01, seed=N + M + gs)
+            x = synth.make_activations(M, L.K, seed=M + 3)
+            y, H = run_prepared(vw, L, x, dora=dora)
+            check_close(y, oracle_product(L, x, H), what=f"N={N} K={K} M={M} gs={gs} dora={dora}")
+
+
 def test_prepared_no_outliers_and_heavy_rows(vw):
     for M in (1, 4, 8):
         _case(M=M, what="no csr")
