@@ -97,6 +97,7 @@ struct StreamArgs {
   int r;
   int M, N, K, S, ng, nch, T, TB;
   uint32_t g_magic;        // floor(c / G) == umulhi(c, g_magic) for c < 2^20
+  int gshift;              // G == 128 << gshift (the kernel's LM == 2 case)
   int splits, cps;         // K splits per tile block, outlier chunks per split
   int spc;                 // slabs per outlier chunk (4; 5 for 3-bit's 640-column chunks)
   int xstride;             // halves per staged activation row
@@ -229,7 +230,9 @@ struct Slab {
   u32x4_t lo, hi;
 };
 
-template <bool PER_ROW, int TPB, int MB>
+// LM: 0 = one LUT per row; 1 = LUT groups of a multiple of 32 columns; 2 = groups of 128 << gshift
+// columns, so a slab's group is s >> gshift for all its lanes (no per-lane group arithmetic).
+template <int LM, int TPB, int MB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MB > 16 ? 4 : WLQ_STREAM_WAVES_PER_EU)))
 void stream4_kernel(const StreamArgs a) {
   constexpr int WPT = 4 / TPB;       // waves per row tile
@@ -316,14 +319,18 @@ void stream4_kernel(const StreamArgs a) {
   const u32x4_t* lb = a.planes + (size_t)t * a.ng * 32 + r;
   auto load_slab = [&](Slab& sl, int s) __attribute__((always_inline)) {
     sl.codes = qb[(size_t)s * 64];
-    if constexpr (!PER_ROW) {
+    if constexpr (LM == 2) {
+      const int g = s >> a.gshift;
+      sl.lo = lb[g * 32];
+      sl.hi = lb[g * 32 + 16];
+    } else if constexpr (LM == 1) {
       const int g = min(group_of(128 * s + 32 * kq, a.g_magic), a.ng - 1);
       sl.lo = lb[g * 32];
       sl.hi = lb[g * 32 + 16];
     }
   };
   LutPlanes<4> pl;
-  if constexpr (PER_ROW) {
+  if constexpr (LM == 0) {
     const u32x4_t lo = lb[0];
     const u32x4_t hi = lb[16];
     pl.lo[0] = lo.x; pl.lo[1] = lo.y; pl.lo[2] = lo.z; pl.lo[3] = lo.w;
@@ -375,7 +382,7 @@ void stream4_kernel(const StreamArgs a) {
   const uint16_t* xrow2 = (NA > 1 && r + 16 < a.M) ? xs + (r + 16) * a.xstride + kq * 32 : nullptr;
   auto consume = [&](const Slab& sl, int s) __attribute__((always_inline)) {
     LutPlanes<4> t4;
-    if constexpr (PER_ROW) {
+    if constexpr (LM == 0) {
       t4 = pl;
     } else {
       t4.lo[0] = sl.lo.x; t4.lo[1] = sl.lo.y; t4.lo[2] = sl.lo.z; t4.lo[3] = sl.lo.w;
@@ -716,9 +723,9 @@ __global__ __launch_bounds__(256) void prep_outliers_kernel(const uint32_t* __re
   }
 }
 
-template <bool PER_ROW, int TPB, int MB>
+template <int LM, int TPB, int MB>
 hipError_t launch_tpl(const StreamArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((stream4_kernel<PER_ROW, TPB, MB>), grid, dim3(256), lds, stream, a);
+  hipLaunchKernelGGL((stream4_kernel<LM, TPB, MB>), grid, dim3(256), lds, stream, a);
   return hipGetLastError();
 }
 
@@ -857,6 +864,10 @@ hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, cons
   const dim3 grid(a.h_blocks + plan.TB * plan.splits);
   const bool per_row = L.group_size <= 0 || lay.ng == 1;
   if (per_row) a.ng = 1;
+  int gshift = 0;
+  while (gshift < 5 && (128 << gshift) < L.group_size) ++gshift;
+  const bool slab_groups = !per_row && L.group_size == (128 << gshift);
+  a.gshift = gshift;
 #define WLQ_STREAM_DISPATCH(PR)                                                  \
   if (plan.tpb == 2) {                                                          \
     if (mb == 1) return launch_tpl<PR, 2, 1>(a, grid, lds, stream);             \
@@ -871,9 +882,11 @@ hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, cons
   if (mb == 16) return launch_tpl<PR, 4, 16>(a, grid, lds, stream);             \
   return launch_tpl<PR, 4, 32>(a, grid, lds, stream);
   if (per_row) {
-    WLQ_STREAM_DISPATCH(true)
+    WLQ_STREAM_DISPATCH(0)
+  } else if (slab_groups) {
+    WLQ_STREAM_DISPATCH(2)
   } else {
-    WLQ_STREAM_DISPATCH(false)
+    WLQ_STREAM_DISPATCH(1)
   }
 #undef WLQ_STREAM_DISPATCH
 }

@@ -51,7 +51,7 @@ def test_prepared_parity(vw, M):
     """M <= 16: one MFMA row group; 17..32: two (rows 16..31 share the dequantized W).
     From M = 16 the reference rounds the GEMM output to fp16 before the DoRA epilogue
     (csrc/vllm_binding.cpp:355-393); the single rounding here is within tolerance of both."""
-    for gs in (0, 32, 64, 128, 256):
+    for gs in (0, 32, 64, 128, 256, 384):  # per row; groups per lane segment; per slab (128 << k); general
         for dora in ("fused", "h", "none"):
             _case(M=M, gs=gs, dora=dora)
             L = synth.make_layer(N=200, K=1408, bits=4, group_size=gs, rank=8, density=0.01, seed=100 + M + gs)
