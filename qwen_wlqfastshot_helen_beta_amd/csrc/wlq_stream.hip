@@ -676,10 +676,18 @@ __global__ __launch_bounds__(256) void prep_planes_kernel(const uint16_t* __rest
     const int n = 16 * t + rr;
     uint32_t w[4] = {0u, 0u, 0u, 0u};
     if (n < N) {
+      // the row's 16 (or 8) fp16 entries as 16-byte loads (rows of 32 / 16 bytes)
       const uint16_t* e = lut + ((size_t)n * ng + g) * nl;
+      uint32_t raw[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+      const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(e);
+      raw[0] = a0.x; raw[1] = a0.y; raw[2] = a0.z; raw[3] = a0.w;
+      if (nl == 16) {
+        const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(e + 8);
+        raw[4] = a1.x; raw[5] = a1.y; raw[6] = a1.z; raw[7] = a1.w;
+      }
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
-        const uint32_t v = k < nl ? (uint32_t)e[k] : 0u;
+        const uint32_t v = (raw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
         const uint32_t b = p ? (v >> 8) : (v & 0xFFu);
         w[k >> 2] |= b << (8 * (k & 3));
       }
