@@ -123,9 +123,10 @@ int wlq_prepare(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K
                 const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz,
                 void* prepared, size_t prepared_bytes, hipStream_t stream);
 
-/* wlq_gemm with the layer's prepared layout: M <= 8 runs the streaming decode
- * kernel on `prepared` (plus the reference chunk offsets), every other case the
- * same kernels as wlq_gemm on the reference-format tensors, which stay required.
+/* wlq_gemm with the layer's prepared layout: M <= 32 runs the streaming decode
+ * kernel on `prepared` (plus the reference chunk offsets) where its activation
+ * staging fits (3-bit: not at M = 13..16 and 26..32), every other case the same
+ * kernels as wlq_gemm on the reference-format tensors, which stay required.
  * Replaces the same reference launchers as wlq_gemm / wlq_gemv
  * (csrc/vllm_binding.cpp:10-52, :318-419). */
 int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c, const void* prepared,
