@@ -274,3 +274,17 @@ def test_create_weights_parameters():
     assert names == {"bits", "ef_bitstream", "ef_tile_meta", "ef_tile_size", "fp8_outliers", "is_quantized", "lut_c",
                      "orig_shape", "outlier_mask", "outlier_mask_1bit", "outlier_values", "outliers", "q_packed",
                      "weight"}, names
+
+
+def test_bench_refuses_multi_gpu_runs():
+    """bench.py measures one GPU: --gpus N > 1 (or a torchrun world) exits with a message, before
+    touching a device."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300)
+    assert r.returncode != 0
+    assert "one GPU" in r.stdout + r.stderr
