@@ -66,7 +66,9 @@ namespace {
 #define WLQ_STREAM_WAVES_PER_EU 5
 #endif
 constexpr int kPF = WLQ_STREAM_PF;  // slabs in flight per wave
-constexpr int kEB = 2;          // outlier entries per thread fetched during the slab loop
+// Outlier entries per thread fetched during the slab loop: 3 where a block covers one or two row
+// tiles (8-16 threads per row; -1-3% at M <= 2), 2 with four tiles (4 threads per row, M > 2).
+template <int TPB> constexpr int outlier_prefetch() { return TPB <= 2 ? 3 : 2; }
 constexpr int kXR = 4;          // 16-byte activation units per thread (the planner bounds the staging)
 constexpr int kHCols = 512;     // columns per DoRA block
 constexpr int kMaxRank = 64;
@@ -362,6 +364,7 @@ void stream4_kernel(const StreamArgs a) {
   }
 
   // Outlier entries, fetched while the slabs stream (clamped, so the loads are unconditional).
+  constexpr int kEB = outlier_prefetch<TPB>();
   uint32_t ecol[kEB];
   float edel[kEB];
   if (csr) {
