@@ -319,16 +319,19 @@ void stream4_kernel(const StreamArgs a) {
   // Slab prefetch.
   const u32x4_t* qb = a.codes + (size_t)t * a.S * 64 + lane;
   const u32x4_t* lb = a.planes + (size_t)t * a.ng * 32 + r;
+  // Codes and LUT planes are read once per call: non-temporal loads keep them from displacing the
+  // activations and DoRA operands that every block re-reads (o_proj at M = 1 8.7 -> 7.9 us).
+  auto ld = [](const u32x4_t* p) __attribute__((always_inline)) { return __builtin_nontemporal_load(p); };
   auto load_slab = [&](Slab& sl, int s) __attribute__((always_inline)) {
-    sl.codes = qb[(size_t)s * 64];
+    sl.codes = ld(qb + (size_t)s * 64);
     if constexpr (LM == 2) {
       const int g = s >> a.gshift;
-      sl.lo = lb[g * 32];
-      sl.hi = lb[g * 32 + 16];
+      sl.lo = ld(lb + g * 32);
+      sl.hi = ld(lb + g * 32 + 16);
     } else if constexpr (LM == 1) {
       const int g = min(group_of(128 * s + 32 * kq, a.g_magic), a.ng - 1);
-      sl.lo = lb[g * 32];
-      sl.hi = lb[g * 32 + 16];
+      sl.lo = ld(lb + g * 32);
+      sl.hi = ld(lb + g * 32 + 16);
     }
   };
   LutPlanes<4> pl;
