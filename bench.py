@@ -85,6 +85,28 @@ def time_graph(g, iters):
     return e0.elapsed_time(e1) / iters
 
 
+def time_windows(run_window, n):
+    """ms of each of n windows (HIP events on the current stream around every call of
+    run_window, all recorded before one synchronization)."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    torch.cuda.synchronize()
+    ev[0].record(stream)
+    for i in range(n):
+        run_window(i)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(n)]
+
+
+def median(v):
+    s = sorted(v)
+    n = len(s)
+    return s[n // 2] if n % 2 else 0.5 * (s[n // 2 - 1] + s[n // 2])
+
+
 PROFILE_SUMMARY = os.path.join(ROOT, "profiles", "decode_gate_up_proj_m1_counters.txt")
 
 
@@ -266,27 +288,42 @@ def main() -> int:
     def layer_fns(c):
         return [(lambda n=n: method.apply(vmods[c][n], xs[vmods[c][n].K])) for n in vnames]
 
+    # exactly --steps steps: full replays of the `copies`-layer graph, then one graph of the
+    # remaining layers; each replay is a timing window, `value` is the median window
     g_layers = graph_of([fn for c in range(copies) for fn in layer_fns(c)])
-    time_graph(g_layers, max(1, args.warmup // copies + 1))
-    replays = max(1, args.steps // copies)
+    full, rem = divmod(max(1, args.steps), copies)
+    g_rem = graph_of([fn for c in range(rem) for fn in layer_fns(c)]) if rem else None
+    warm_full, warm_rem = divmod(max(0, args.warmup), copies)
+    for _ in range(warm_full):
+        g_layers.replay()
+    if warm_rem:
+        graph_of([fn for c in range(warm_rem) for fn in layer_fns(c)]).replay()
+    torch.cuda.synchronize()
+    windows = [g_layers] * full + ([g_rem] if g_rem is not None else [])
     wall0 = time.perf_counter()
-    ms_step = time_graph(g_layers, replays) / copies
+    win_ms = time_windows(lambda i: windows[i].replay(), len(windows))
     wall = time.perf_counter() - wall0
-    steps_timed = replays * copies
+    steps_timed = full * copies + rem
+    per_step = [w / copies for w in win_ms[:full]] or [win_ms[-1] / rem]
+    ms_step = median(per_step)
+    ms_step_mean = sum(win_ms) / steps_timed
     value = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"[bench] layer step {ms_step * 1e3:.2f} us -> {value:.0f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of HBM peak),"
-        f" wall {wall:.3f}s for {steps_timed} steps")
+    log(f"[bench] layer step {ms_step * 1e3:.2f} us (median of {len(per_step)} windows; mean {ms_step_mean * 1e3:.2f} us)"
+        f" -> {value:.0f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of HBM peak), wall {wall:.3f}s for {steps_timed} steps")
 
     # ---- per-shape products: `copies` launches of one product in one graph
-    def op_time(L, M, reps=20):
-        mods = [attach_synthetic(torch.nn.Module(), L, dev, prepared=prep) for _ in range(copies)]
+    def op_time(L, M, launches=100):
+        """Median per-launch time of one product: a graph of `nc` launches on rotating weight
+        copies, replayed until >= `launches` launches are timed, one window per replay."""
+        nc = copies if M <= 32 else 4  # M > 32 re-reads the weights M/256 times inside one product anyway
+        mods = [attach_synthetic(torch.nn.Module(), L, dev, prepared=prep) for _ in range(nc)]
         xm = torch.randn(M, L.K, device=dev).half()
         out = torch.empty(M, L.N, device=dev, dtype=torch.float16)
         g = graph_of([op_fn(m, L, xm, out) for m in mods])
         time_graph(g, 2)
-        ms = time_graph(g, reps) / copies
+        w = time_windows(lambda i: g.replay(), max(3, math.ceil(launches / nc)))
         del g, mods
-        return ms
+        return median(w) / nc
 
     per_shape = {}
     Ms = [1] if args.no_sweep else [1, 4, 8, 16, 32]
@@ -304,23 +341,20 @@ def main() -> int:
     # dominant kernel: its average launch duration over back-to-back eager launches (HIP events on
     # the launch stream around the timed region, as under rocprofv3's --op run); still includes the
     # ~2 us gap between consecutive kernels of one stream that the profiler's kernel time excludes
-    def kernel_time(L, M, reps=60):
+    def kernel_time(L, M, windows=15):
         mods = [attach_synthetic(torch.nn.Module(), L, dev, prepared=prep) for _ in range(copies)]
         xm = torch.randn(M, L.K, device=dev).half()
         out = torch.empty(M, L.N, device=dev, dtype=torch.float16)
         fns = [op_fn(m, L, xm, out) for m in mods]
         for i in range(2 * copies):
             fns[i % copies]()
-        stream = torch.cuda.current_stream()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for i in range(reps):
-            fns[i % copies]()
-        e1.record(stream)
-        torch.cuda.synchronize()
+
+        def window(_):
+            for f in fns:
+                f()
+        w = time_windows(window, windows)
         del mods
-        return e0.elapsed_time(e1) / reps
+        return median(w) / copies
 
     dom_ms = kernel_time(merged["gate_up_proj"], 1)
     dom_gbs = merged["gate_up_proj"].headline_bytes() / (dom_ms * 1e-3) / 1e9
@@ -332,37 +366,36 @@ def main() -> int:
                            "skinny4_kernel (row-aligned layout") +
                           "; decode product incl. DoRA x.A^T blocks and in-kernel epilogue), gate_up_proj 37888x3584 M=1",
                 "bytes_per_launch": merged["gate_up_proj"].headline_bytes(), "avg_us": dom["us"],
-                "timing": "60 back-to-back eager launches, HIP events on the launch stream",
+                "timing": "median of 15 windows of back-to-back eager launches (one per weight copy), HIP events on "
+                          "the launch stream",
                 "graph_avg_us": per_shape["gate_up_proj_M1"]["us"]}
 
-    # ---- prefill GEMM, M = 128 (config 2, the ridge: both fractions) and M = 2048
-    gemm = gemm128 = None
+    # ---- prefill GEMM (config 2): the seven shapes at M = 128 (the ridge: both the MFMA and the
+    # HBM fraction), 512, 2048 (the headline's TFLOP/s figure) and 8192
+    gemm = gemm128 = cfg2 = None
     if not args.no_gemm:
-        rows128 = {}
-        for n in names:
-            L = layers[n]
-            ms = op_time(L, 128, reps=5)
-            fl = 2.0 * 128 * L.N * L.K
-            tf = fl / (ms * 1e-3) / 1e12
-            gbs = L.headline_bytes() / (ms * 1e-3) / 1e9
-            rows128[n] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
-                          "frac_mfma": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "GB/s": round(gbs, 1),
-                          "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-            log(f"[bench] gemm {n:9s} M=128: {ms * 1e3:8.1f} us  {tf:7.1f} TFLOP/s  {gbs:7.0f} GB/s")
-        gemm128 = {"M": 128, "per_shape": rows128}
-        M = 2048
-        tot_flop, tot_ms, rows = 0.0, 0.0, {}
-        for n in names:
-            L = layers[n]
-            ms = op_time(L, M, reps=3)
-            fl = 2.0 * M * L.N * L.K
-            tot_flop += fl
-            tot_ms += ms
-            rows[n] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(fl / (ms * 1e-3) / 1e12, 1)}
-            log(f"[bench] gemm {n:9s} M={M}: {ms * 1e3:8.1f} us  {rows[n]['TFLOP/s']:7.1f} TFLOP/s")
-        tf = tot_flop / (tot_ms * 1e-3) / 1e12
-        gemm = {"M": M, "TFLOP/s": round(tf, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
-                "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "per_shape": rows}
+        cfg2 = {}
+        for M in (128, 512, 2048, 8192):
+            tot_flop, tot_ms, rows = 0.0, 0.0, {}
+            for n in names:
+                L = layers[n]
+                ms = op_time(L, M, launches=100 if M <= 2048 else 40)
+                fl = 2.0 * M * L.N * L.K
+                tf = fl / (ms * 1e-3) / 1e12
+                tot_flop += fl
+                tot_ms += ms
+                rows[n] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 1),
+                           "frac_mfma": round(tf / MFMA_FP16_PEAK_TFLOPS, 4)}
+                if M == 128:
+                    gbs = L.headline_bytes() / (ms * 1e-3) / 1e9
+                    rows[n].update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+                log(f"[bench] gemm {n:9s} M={M:4d}: {ms * 1e3:8.1f} us  {tf:7.1f} TFLOP/s")
+            tf = tot_flop / (tot_ms * 1e-3) / 1e12
+            cfg2[f"M{M}"] = {"M": M, "TFLOP/s": round(tf, 1), "peak": MFMA_FP16_PEAK_TFLOPS,
+                             "frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "per_shape": rows}
+            log(f"[bench] gemm M={M}: {tf:.1f} TFLOP/s aggregate over the seven shapes")
+        gemm = cfg2["M2048"]
+        gemm128 = cfg2["M128"]
 
     # ---- config 3: outlier / adapter stress on gate_proj at M = 1 and M = 512, one factor at a time
     # around the base case (d = 0.5%, r = 16, G = 128, 4-bit); 20% of rows are heavy (10x the
@@ -382,7 +415,7 @@ def main() -> int:
             L = synth.make_layer(*synth.QWEN25_7B_SHAPES["gate_proj"], seed=30, heavy_frac=0.2, heavy_mult=10, **kw)
             row = dict(kw)
             for M in (1, 512):
-                ms = op_time(L, M, reps=5)
+                ms = op_time(L, M, launches=100)
                 if M == 1:
                     gbs = L.headline_bytes() / (ms * 1e-3) / 1e9
                     row["M1"] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
@@ -424,6 +457,8 @@ def main() -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps_timed,
+        "timing": {"windows": len(win_ms), "steps_per_window": copies, "ms_per_step_mean": round(ms_step_mean, 5),
+                   "ms_per_step_min": round(min(per_step), 5), "ms_per_step_max": round(max(per_step), 5)},
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
@@ -441,6 +476,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "gemm_m2048": gemm,
         "gemm_m128": gemm128,
+        "cfg2": cfg2,
         "cfg3": cfg3,
         "box_peaks": box,
         "per_shape": per_shape,

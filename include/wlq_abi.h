@@ -41,6 +41,14 @@
  * reduced to what fits.  No workspace is valid unless H has to be computed
  * from lora_A (then WLQ_ERR_CAPACITY reports the minimum).  Calls that share
  * one workspace must be ordered on one stream.
+ *
+ * Failed hand-offs are reported, not hidden: a kernel that finds a counter beyond
+ * what one call can reach (the area was not zero at entry, e.g. two unordered
+ * calls on one workspace) or whose wait for the fused DoRA H runs out of polls
+ * (~1 s) sets a sticky error word at the end of the counter area and writes the
+ * rows concerned as fp16 NaN.  While the word is set every call on the
+ * workspace writes NaN rows.  wlq_workspace_status reports it, and
+ * wlq_workspace_reset clears the counter area.
  */
 #ifndef WLQ_ABI_H
 #define WLQ_ABI_H
@@ -54,7 +62,7 @@
 extern "C" {
 #endif
 
-#define WLQ_ABI_VERSION 4
+#define WLQ_ABI_VERSION 5
 
 enum wlq_status {
   WLQ_OK = 0,
@@ -63,7 +71,8 @@ enum wlq_status {
   WLQ_ERR_UNSUPPORTED = 3,  /* bits or group_size outside the supported set */
   WLQ_ERR_CAPACITY = 4,     /* an output buffer is too small */
   WLQ_ERR_HIP = 5,          /* the HIP runtime reported an error */
-  WLQ_ERR_FORMAT = 6        /* malformed input stream */
+  WLQ_ERR_FORMAT = 6,       /* malformed input stream */
+  WLQ_ERR_SYNC = 7          /* a cross-block hand-off on a workspace failed (see wlq_workspace_status) */
 };
 
 int wlq_abi_version(void);
@@ -103,6 +112,22 @@ int wlq_gemm(const void* X, const int32_t* q_packed, const void* lut_c, void* ou
              const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals,
              const float* lora_H, const void* lora_B, const void* dora_gamma, const void* lora_A,
              float lora_scale, int32_t r, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Host: wait for `stream`, then read the workspace's sticky error word.  WLQ_OK
+ * when no hand-off failed on it (also when workspace_bytes is below the 16 KiB
+ * counter area, which then holds no counters), else WLQ_ERR_SYNC with the failure
+ * in wlq_last_error().  Synchronizes: not for use inside graph capture.
+ * No reference counterpart: the reference's split-K reduce is a second kernel with no
+ * cross-block waits (csrc/gemv_kernel.cu:322-353, :449-456). */
+int wlq_workspace_status(const void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Device: zero the workspace's counter area (counters and error word) on `stream`
+ * with a fill kernel (graph-safe, no hipMemset).  Use once after allocating a
+ * workspace, or after wlq_workspace_status reported WLQ_ERR_SYNC and the calls
+ * that used the workspace have finished.  No reference counterpart (see above);
+ * it takes the place of the reference's zero-initialised workspace tensors
+ * (csrc/vllm_binding.cpp:238-251). */
+int wlq_workspace_reset(void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Bytes of the prepared (tile-contiguous) layout of a layer, or 0 when the
  * layer has none (it needs 4-bit or 3-bit codes, a per-row LUT or a group size that is a

@@ -57,6 +57,8 @@ def _declare(lib: ctypes.CDLL) -> None:
                                              vp, vp, c_i64, vp, vp, vp, vp, c_f, c_i32, vp, c_sz, vp]),
         "wlq_dequant": (ctypes.c_int, [vp, vp, vp, c_i64, c_i64, c_i32, c_i64, c_i32, vp, vp, vp, vp]),
         "wlq_dora_epilogue": (ctypes.c_int, [vp, vp, vp, vp, c_f, c_i32, c_i64, c_i64, vp]),
+        "wlq_workspace_status": (ctypes.c_int, [vp, c_sz, vp]),
+        "wlq_workspace_reset": (ctypes.c_int, [vp, c_sz, vp]),
         "wlq_repack_row_aligned": (ctypes.c_int, [vp, c_i64, c_i64, c_i64, c_i32, vp, c_i64]),
         "wlq_ef_total": (c_i64, [vp, c_i64]),
         "wlq_ef_decode_chunk_csr": (ctypes.c_int, [vp, c_i64, vp, c_i64, c_i64, c_i64, c_i64, c_i64, vp, vp, c_i64,

@@ -12,13 +12,15 @@
 //
 // Differences from the reference, all stricter: dtypes, devices, contiguity and
 // sizes are checked before launch, unsupported bit widths raise instead of
-// silently doing nothing, and the split-K workspace is kept per device.
+// silently doing nothing, and the split-K workspace is kept per (device, stream).
 #include <torch/extension.h>
 
 #include <c10/hip/HIPStream.h>
 
+#include <map>
 #include <mutex>
-#include <unordered_map>
+#include <utility>
+#include <vector>
 
 #include "wlq_abi.h"
 
@@ -73,18 +75,57 @@ void check_csr(const c10::optional<torch::Tensor>& offs, const c10::optional<tor
     TORCH_CHECK(cols->numel() == vals->numel(), "chunk_cols and chunk_vals differ in length");
 }
 
-// Split-K workspace, one per device, grown on demand (csrc/vllm_binding.cpp:238-251).
-std::mutex g_ws_mu;
-std::unordered_map<int, torch::Tensor> g_ws;
+// Workspaces (counter area + split-K / DoRA partial sums), one per (device, stream):
+// the decode kernels hand partial results between blocks through the workspace, so
+// two calls on one workspace must be ordered, and only calls on the same stream are
+// (csrc/vllm_binding.cpp:238-251 keeps one per process, shared by every stream).
+// init_workspaces sets a per-device size floor.  A stream's workspace is created (or
+// replaced by a larger one) on demand; its 16 KiB counter area is zeroed by a fill
+// kernel on that stream.  Replaced workspaces are never freed, since captured graphs
+// may still use them.  Created while the stream is being captured, the fill kernel
+// is only recorded (every replay of the graph runs it first), so the workspace is
+// zeroed again before its next eager call.
+constexpr size_t kCounterBytes = 16384;
 
-torch::Tensor workspace_for(const torch::Device& dev, size_t bytes) {
-  std::lock_guard<std::mutex> lk(g_ws_mu);
-  auto& t = g_ws[dev.index()];
-  if (!t.defined() || (size_t)t.numel() < bytes) {
-    // zero-filled: the leading arrival counters must start at zero (calls leave them zero)
-    t = torch::zeros({(int64_t)std::max<size_t>(bytes, 256)}, torch::TensorOptions().dtype(torch::kUInt8).device(dev));
+struct Workspace {
+  torch::Tensor buf;
+  bool zero_before_eager = false;
+  bool captured = false;  // handed to a call under graph capture: never freed
+};
+
+std::mutex g_ws_mu;
+std::map<std::pair<int, uintptr_t>, Workspace> g_ws;
+std::map<int, size_t> g_ws_floor;
+std::vector<torch::Tensor> g_ws_retired;
+
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
   }
-  return t;
+  return st != hipStreamCaptureStatusNone;
+}
+
+// `stream` is torch's current stream on `dev` (the allocation and the fill run on it).
+torch::Tensor workspace_for(const torch::Device& dev, size_t bytes, hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  bytes = std::max({bytes, g_ws_floor[dev.index()], kCounterBytes});
+  Workspace& w = g_ws[{dev.index(), reinterpret_cast<uintptr_t>(stream)}];
+  const bool capturing = stream_capturing(stream);
+  if (!w.buf.defined() || (size_t)w.buf.numel() < bytes) {
+    // a buffer only eager calls used is released to torch's allocator (stream-ordered on `stream`)
+    if (w.buf.defined() && w.captured) g_ws_retired.push_back(w.buf);
+    w.buf = torch::empty({(int64_t)bytes}, torch::TensorOptions().dtype(torch::kUInt8).device(dev));
+    w.buf.narrow(0, 0, (int64_t)kCounterBytes).zero_();  // a fill kernel (valid inside graph capture)
+    w.zero_before_eager = capturing;
+    w.captured = false;
+  } else if (w.zero_before_eager && !capturing) {
+    w.buf.narrow(0, 0, (int64_t)kCounterBytes).zero_();
+    w.zero_before_eager = false;
+  }
+  w.captured = w.captured || capturing;
+  return w.buf;
 }
 
 hipStream_t current_stream(const torch::Device& dev) { return c10::hip::getCurrentHIPStream(dev.index()).stream(); }
@@ -114,7 +155,36 @@ void init_workspaces(int64_t max_N, int64_t max_K, torch::Device device) {
     for (int64_t M = 64; M <= 16384; M *= 2)
       need = std::max(need, wlq_gemm_workspace_bytes(M, max_N, max_K, bits, 0, device.index()));
   }
-  workspace_for(device, need);
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    size_t& f = g_ws_floor[device.index()];
+    f = std::max(f, need);
+  }
+  workspace_for(device, need, current_stream(device));
+}
+
+// Raises when a cross-block hand-off failed on any workspace of `device` (the rows
+// concerned were written as NaN); waits for the streams of those workspaces.
+void check_workspaces(torch::Device device) {
+  std::vector<std::pair<uintptr_t, torch::Tensor>> ws;
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (auto& kv : g_ws)
+      if (kv.first.first == device.index()) ws.emplace_back(kv.first.second, kv.second.buf);
+  }
+  for (auto& w : ws)
+    check_status(wlq_workspace_status(w.second.data_ptr(), (size_t)w.second.numel(),
+                                      reinterpret_cast<hipStream_t>(w.first)));
+}
+
+// Clears the counter area of every workspace of `device` on its own stream (after a
+// reported failure, once the calls that used them are done).
+void reset_workspaces(torch::Device device) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  for (auto& kv : g_ws)
+    if (kv.first.first == device.index())
+      check_status(wlq_workspace_reset(kv.second.buf.data_ptr(), (size_t)kv.second.buf.numel(),
+                                       reinterpret_cast<hipStream_t>(kv.first.second)));
 }
 
 void gemv_forward(torch::Tensor q_packed, torch::Tensor lut_c, torch::Tensor x, torch::Tensor out, int64_t N,
@@ -149,7 +219,7 @@ void gemv_forward(torch::Tensor q_packed, torch::Tensor lut_c, torch::Tensor x, 
     TORCH_CHECK(dora_gamma->numel() == N, "dora_gamma must have N elements");
   }
   const size_t need = wlq_gemm_workspace_bytes(1, N, K, (int32_t)bits, (h || !A) ? 0 : r, dev.index());
-  torch::Tensor ws = workspace_for(dev, need);
+  torch::Tensor ws = workspace_for(dev, need, current_stream(dev));
   const void* prep = prepared_ptr(prepared, dev);
   if (prep != nullptr) {
     check_status(wlq_gemm_prepared(x.data_ptr(), q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), prep,
@@ -197,7 +267,7 @@ void gemm_forward(torch::Tensor X, torch::Tensor q_packed, torch::Tensor lut_c, 
     TORCH_CHECK(dora_gamma->numel() == N, "dora_gamma must have N elements");
   }
   const size_t need = wlq_gemm_workspace_bytes(M, N, K, (int32_t)bits, (H || !A) ? 0 : r, dev.index());
-  torch::Tensor ws = workspace_for(dev, need);
+  torch::Tensor ws = workspace_for(dev, need, current_stream(dev));
   const void* prep = prepared_ptr(prepared, dev);
   if (prep != nullptr) {
     check_status(wlq_gemm_prepared(X.data_ptr(), q_packed.data_ptr<int32_t>(), lut_c.data_ptr(), prep,
@@ -306,6 +376,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("bits"));
   m.def("init_workspaces", &init_workspaces, "Pre-size the split-K workspace for graph capture", py::arg("max_N"),
         py::arg("max_K"), py::arg("device"));
+  m.def("check_workspaces", &check_workspaces,
+        "Raise if a cross-block hand-off failed on a workspace of the device (waits for its streams)",
+        py::arg("device"));
+  m.def("reset_workspaces", &reset_workspaces, "Clear the counter area of every workspace of the device",
+        py::arg("device"));
   m.def("gemv_forward", &gemv_forward, "WLQ decode product (one activation row)", py::arg("q_packed"),
         py::arg("lut_c"), py::arg("x"), py::arg("out"), py::arg("N"), py::arg("K"), py::arg("bits"),
         py::arg("chunk_offsets") = py::none(), py::arg("chunk_cols") = py::none(), py::arg("chunk_vals") = py::none(),

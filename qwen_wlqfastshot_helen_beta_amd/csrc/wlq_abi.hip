@@ -8,6 +8,7 @@
 // device's value for all devices, csrc/gemv_kernel.cu:355-363).
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 
 #include "wlq_abi.h"
 #include "wlq_internal.h"
@@ -17,7 +18,45 @@ void set_error(const char* fmt, ...);
 int window_cols_for(int bits);
 }  // namespace wlq
 
+namespace wlq {
+
 namespace {
+// 0: not read yet, 1: hooks off, 2: hooks on (WLQ_TEST_HOOKS=1 at the first product)
+std::atomic<int> g_hooks{0};
+
+bool hooks_on() {
+  int h = g_hooks.load(std::memory_order_relaxed);
+  if (h == 0) {
+    const char* e = std::getenv("WLQ_TEST_HOOKS");
+    h = (e != nullptr && e[0] == '1') ? 2 : 1;
+    g_hooks.store(h, std::memory_order_relaxed);
+  }
+  return h == 2;
+}
+}  // namespace
+
+uint32_t spin_limit() {
+  if (hooks_on()) {
+    const char* e = std::getenv("WLQ_SPIN_LIMIT");
+    if (e != nullptr && e[0] != 0) return (uint32_t)std::strtoul(e, nullptr, 10);
+  }
+  return kDefaultSpinLimit;
+}
+
+bool withhold_h() {
+  if (!hooks_on()) return false;
+  const char* e = std::getenv("WLQ_TEST_WITHHOLD_H");
+  return e != nullptr && e[0] == '1';
+}
+
+}  // namespace wlq
+
+namespace {
+
+// Clears `words` 32-bit words (the counter area) with plain vector stores.
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int words) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < words; i += gridDim.x * 256) p[i] = 0u;
+}
 
 constexpr int kMaxDevices = 64;
 std::atomic<int> g_cu_count[kMaxDevices];
@@ -318,6 +357,40 @@ int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c,
     }
   }
   return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, "wlq_gemm_prepared");
+}
+
+int wlq_workspace_status(const void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (workspace == nullptr || workspace_bytes < wlq::kSyncBytes) return WLQ_OK;
+  int st = hip_status(hipStreamSynchronize(stream), "wlq_workspace_status");
+  if (st != WLQ_OK) return st;
+  uint32_t err = 0;
+  st = hip_status(hipMemcpy(&err, reinterpret_cast<const uint32_t*>(workspace) + wlq::kSyncErrorWord, sizeof(err),
+                            hipMemcpyDeviceToHost),
+                  "wlq_workspace_status");
+  if (st != WLQ_OK) return st;
+  if (err == 0) return WLQ_OK;
+  wlq::set_error("wlq_workspace_status: hand-off failures on this workspace (error word 0x%x:%s%s); the rows concerned "
+                 "and every later call's rows were written as NaN; clear it with wlq_workspace_reset",
+                 err, (err & wlq::kErrHTimeout) ? " a wait for the DoRA H ran out of polls;" : "",
+                 (err & wlq::kErrArrivals) ? " a counter exceeded one call's arrivals (not zero at entry: unordered "
+                                             "calls on one workspace, or never zero-filled);" : "");
+  return WLQ_ERR_SYNC;
+}
+
+int wlq_workspace_reset(void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (workspace == nullptr) {
+    wlq::set_error("wlq_workspace_reset: workspace must be non-null");
+    return WLQ_ERR_NULL_POINTER;
+  }
+  if ((reinterpret_cast<uintptr_t>(workspace) & 3u) != 0) {
+    wlq::set_error("wlq_workspace_reset: workspace must be 4-byte aligned");
+    return WLQ_ERR_BAD_SHAPE;
+  }
+  const int words = (int)(std::min(workspace_bytes, wlq::kSyncBytes) / 4);
+  if (words == 0) return WLQ_OK;
+  hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, stream,
+                     reinterpret_cast<uint32_t*>(workspace), words);
+  return hip_status(hipGetLastError(), "wlq_workspace_reset");
 }
 
 int wlq_dequant(const int32_t* q_packed, const void* lut_c, void* W_out, int64_t N, int64_t K, int32_t bits,

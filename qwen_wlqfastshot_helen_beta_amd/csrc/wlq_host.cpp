@@ -43,6 +43,7 @@ const char* wlq_status_string(int status) {
     case WLQ_ERR_CAPACITY: return "insufficient capacity";
     case WLQ_ERR_HIP: return "HIP error";
     case WLQ_ERR_FORMAT: return "malformed input";
+    case WLQ_ERR_SYNC: return "cross-block hand-off failed (outputs written as NaN)";
     default: return "unknown status";
   }
 }

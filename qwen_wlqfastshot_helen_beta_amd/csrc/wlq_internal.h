@@ -44,7 +44,23 @@ struct SplitPlan {
 // on a workspace and every call leaves them zero.  Products, H and partials use the
 // bytes after them.
 constexpr size_t kSyncBytes = 16384;
-constexpr int kMaxSyncRowBlocks = (int)(kSyncBytes / 4);
+constexpr int kSyncWords = (int)(kSyncBytes / 4);
+// The area's last 128-byte line holds the sticky error word (the counters use the words
+// before it).  A kernel that detects a failed hand-off ORs one of the kErr* bits into it
+// and writes the rows concerned as fp16 NaN; later calls on the workspace see the word
+// and write NaN too, until wlq_workspace_reset clears the area.
+constexpr int kSyncErrorWord = kSyncWords - 32;
+constexpr int kMaxSyncRowBlocks = kSyncErrorWord;
+constexpr uint32_t kErrHTimeout = 1u;   // a wait for the DoRA H ran out of polls
+constexpr uint32_t kErrArrivals = 2u;   // an arrival count exceeded what one call makes
+constexpr uint32_t kDefaultSpinLimit = 1u << 24;  // ~1 s of polls
+
+// Polls of a ready slot before a wait gives up (default kDefaultSpinLimit), and the
+// test hook that keeps the DoRA finisher from raising its ready slots.  Both come from
+// the environment only when WLQ_TEST_HOOKS=1 was set when the library first ran a
+// product (WLQ_SPIN_LIMIT, WLQ_TEST_WITHHOLD_H, read on every call then).
+uint32_t spin_limit();
+bool withhold_h();
 
 int slab_cols(int bits);             // columns one 16-row wave tile covers per step
 int skinny_max_m();

@@ -96,6 +96,13 @@ __device__ __forceinline__ float load_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void fence_release() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ uint32_t load_dev(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void raise_error(uint32_t* sync, uint32_t bit) {
+  __hip_atomic_fetch_or(sync + kSyncErrorWord, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr uint16_t kHalfNaN = 0x7E00u;
 __device__ __forceinline__ void fence_acquire() { asm volatile("" ::: "memory"); }
 
 __device__ __forceinline__ int group_of(int col, uint32_t magic) { return (int)__umulhi((uint32_t)col, magic); }
@@ -292,6 +299,9 @@ __device__ __forceinline__ float sum_dev(const float* p, size_t stride, int n_te
 // blocks are summed in index order, so the result does not depend on arrival order.
 // lds: at least M * r free floats.
 __device__ __forceinline__ void finish_rows(const SkinnyArgs& a, int rb0, const int* rbs, int count, float* lds) {
+  // NaN rows when a hand-off on this workspace failed (this call or an earlier one): the
+  // sticky error word of the counter area
+  const bool poisoned = load_dev(a.sync + kSyncErrorWord) != 0u;
   const float* h = a.H;
   if (a.r > 0 && a.hpart != nullptr) {
     for (int idx = threadIdx.x; idx < a.M * a.r; idx += blockDim.x)
@@ -328,7 +338,7 @@ __device__ __forceinline__ void finish_rows(const SkinnyArgs& a, int rb0, const 
       }
       v = (v + a.scale * ls) * h2f(a.gamma[n]);
     }
-    a.out[idx] = f2h_rn(v);
+    a.out[idx] = poisoned ? kHalfNaN : f2h_rn(v);
   }
 }
 
@@ -338,7 +348,11 @@ __device__ __forceinline__ void arrive_product(const SkinnyArgs& a, int rb, floa
   __shared__ int s_last;
   fence_release();  // this block's partial stores are complete before it counts
   __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(a.sync + rb, 1u) == (uint32_t)(a.arrivals - 1);
+  if (threadIdx.x == 0) {
+    const uint32_t old = atomicAdd(a.sync + rb, 1u);
+    if (old >= (uint32_t)a.arrivals) raise_error(a.sync, kErrArrivals);  // counters not zero at entry
+    s_last = old >= (uint32_t)(a.arrivals - 1);  // an overflowing block finishes too (with NaN rows)
+  }
   __syncthreads();
   if (!s_last) return;
   fence_acquire();
@@ -362,6 +376,7 @@ __device__ __forceinline__ bool finish_direct(const SkinnyArgs& a, int rb, int n
   __syncthreads();
   if (!s_ready) return false;
   fence_acquire();
+  const bool poisoned = load_dev(a.sync + kSyncErrorWord) != 0u;
   for (int idx = threadIdx.x; idx < a.M * a.r; idx += blockDim.x)
     lds[idx] = h2f(f2h_rn(sum_dev(a.hpart + idx, (size_t)a.M * a.r, a.h_blocks)));
   __syncthreads();
@@ -375,7 +390,7 @@ __device__ __forceinline__ bool finish_direct(const SkinnyArgs& a, int rb, int n
         const float* hi = lds + (size_t)i * a.r;
         const uint16_t* bb = a.B + (size_t)n * a.r;
         for (int j = 0; j < a.r; ++j) ls += hi[j] * h2f(bb[j]);
-        a.out[(size_t)i * a.N + n] = f2h_rn((acc[mt][e] + a.scale * ls) * h2f(a.gamma[n]));
+        a.out[(size_t)i * a.N + n] = poisoned ? kHalfNaN : f2h_rn((acc[mt][e] + a.scale * ls) * h2f(a.gamma[n]));
       }
     }
   }
@@ -391,8 +406,11 @@ __device__ __forceinline__ void arrive_dora(const SkinnyArgs& a, float* lds) {
     if (threadIdx.x == 0) s_n = 0;
     __syncthreads();
     const int rb = base + (int)threadIdx.x;
-    if (rb < a.row_blocks && atomicAdd(a.sync + rb, 1u) == (uint32_t)(a.arrivals - 1))
-      s_list[atomicAdd(&s_n, 1)] = rb;
+    if (rb < a.row_blocks) {
+      const uint32_t old = atomicAdd(a.sync + rb, 1u);
+      if (old >= (uint32_t)a.arrivals) raise_error(a.sync, kErrArrivals);  // counters not zero at entry
+      if (old >= (uint32_t)(a.arrivals - 1)) s_list[atomicAdd(&s_n, 1)] = rb;
+    }
     __syncthreads();
     const int cnt = s_n;
     if (cnt > 0) {

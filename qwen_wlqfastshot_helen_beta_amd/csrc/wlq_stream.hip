@@ -45,6 +45,14 @@
 // flag; a block that needs H waits for the flag (normally long set by then).  The
 // last block to finish resets the flag and the counters, so every call leaves
 // them zero.
+//
+// Failures of the hand-off are loud, not silent.  A wait for H that runs out of
+// polls, or an arrival count that exceeds the number of arrivals a call can make
+// (the counters were not zero at entry: a workspace shared by unordered calls,
+// or never zero-filled), sets a bit in the workspace's error word and the rows
+// concerned are written as fp16 NaN.  The error word is sticky: every later call
+// on that workspace writes NaN rows too, until the host reads it
+// (wlq_workspace_status) and clears the counter area (wlq_workspace_reset).
 #include <algorithm>
 
 #include "wlq_device.h"
@@ -74,10 +82,9 @@ constexpr int kHCols = 512;     // columns per DoRA block
 constexpr int kMaxRank = 64;
 constexpr int kXBudget = 16384; // activation staging bytes per block
 constexpr int kBlocksPerCU = WLQ_STREAM_BLOCKS_PER_CU;  // tile-block target per CU
-constexpr uint32_t kSpinLimit = 1u << 24;
-
 // Sync words in the workspace's counter area (all zero between calls).
 constexpr int kSyncDora = 0;      // DoRA blocks arrived (reset by the last of them)
+constexpr int kSyncErr = kSyncErrorWord;  // sticky error bits (own 128-byte line)
 constexpr int kSyncSlot0 = 64;    // ready slots: word 0 = H published, word 1 = consumers counted
 constexpr int kSlotWords = 16;    // one 64-byte line per slot
 constexpr int kMaxSlots = 128;    // tile block tb uses slot tb % min(TB, kMaxSlots)
@@ -108,7 +115,15 @@ struct StreamArgs {
   float* hpart;            // [h_blocks, M, r]
   float* hfin;             // [M, r]
   uint32_t* sync;
+  uint32_t spin_limit;     // polls of a ready slot before the wait gives up
+  int withhold_h;          // test hook: the DoRA finisher never raises the ready slots
 };
+
+// Error word: bits from wlq_internal.h (kErr*), set with a device-scope atomic OR.
+__device__ __forceinline__ void raise_error(uint32_t* sync, uint32_t bit) {
+  __hip_atomic_fetch_or(sync + kSyncErr, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr uint16_t kHalfNaN = 0x7E00u;
 
 __device__ __forceinline__ void store_dev(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -200,7 +215,11 @@ __device__ void dora_block(const StreamArgs& a, int hb, float* red) {
   stores_done();
   __syncthreads();
   __shared__ int s_last;
-  if (threadIdx.x == 0) s_last = atomicAdd(a.sync + kSyncDora, 1u) == (uint32_t)(a.h_blocks - 1);
+  if (threadIdx.x == 0) {
+    const uint32_t old = atomicAdd(a.sync + kSyncDora, 1u);
+    if (old >= (uint32_t)a.h_blocks) raise_error(a.sync, kErrArrivals);  // no finisher: the H waits run out
+    s_last = old == (uint32_t)(a.h_blocks - 1);
+  }
   __syncthreads();
   if (!s_last) return;
   compiler_fence();
@@ -221,7 +240,8 @@ __device__ void dora_block(const StreamArgs& a, int hb, float* red) {
   __syncthreads();
   // H is visible: raise every ready slot, then reset the arrival count for the next call
   const int slots = min(a.TB, kMaxSlots);
-  for (int g = threadIdx.x; g < slots; g += blockDim.x) store_dev(a.sync + kSyncSlot0 + kSlotWords * g, 1u);
+  if (!a.withhold_h)
+    for (int g = threadIdx.x; g < slots; g += blockDim.x) store_dev(a.sync + kSyncSlot0 + kSlotWords * g, 1u);
   if (threadIdx.x == 0) store_dev(a.sync + kSyncDora, 0u);
 }
 
@@ -276,6 +296,12 @@ void stream4_kernel(const StreamArgs a) {
   float* hs = reinterpret_cast<float*>(smem);
   uint16_t* bs = reinterpret_cast<uint16_t*>(red + 4 * NA * 256);
   uint16_t* gs = bs + ROWS * a.r;
+
+  // Sticky error of an earlier call (loaded now, used by the epilogue) and this call's own.
+  __shared__ int s_err;
+  uint32_t err0 = 0;
+  if (a.sync != nullptr) err0 = load_dev(a.sync + kSyncErr);
+  if (threadIdx.x == 0) s_err = 0;
 
   // Outlier pass mapping: thread (rho, j) walks entries j, j + TPR, ... of block row rho.
   const int rho = threadIdx.x / TPR;
@@ -444,9 +470,10 @@ void stream4_kernel(const StreamArgs a) {
   // DoRA H into registers.  A caller's H, or (one K split: this block finishes its rows) the
   // computed H, is loaded now so the loads complete while the outlier pass runs; with several
   // splits only the last to arrive needs H and loads it then.  Computed H: each wave first
-  // waits for the block's ready slot (normally raised long before; cut off after kSpinLimit
-  // polls rather than hang).  A block polls before it counts itself on the slot, so no slot is
-  // lowered while one of its tile blocks still polls.
+  // waits for the block's ready slot (normally raised long before; after spin_limit polls the
+  // wait gives up, raises kErrHTimeout and the block writes NaN rows rather than hang).  A
+  // block polls before it counts itself on the slot, so no slot is lowered while one of its
+  // tile blocks still polls.
   const int slots = min(a.TB, kMaxSlots);
   uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
   constexpr int kHB = (MB * kMaxRank + 255) / 256;  // H words per thread (M * r <= MB * 64)
@@ -454,7 +481,15 @@ void stream4_kernel(const StreamArgs a) {
   auto load_h = [&]() __attribute__((always_inline)) {
     if (a.h_blocks > 0) {
       if (lane == 0) {
-        for (uint32_t spins = 0; load_dev(slot) == 0u && spins < kSpinLimit; ++spins) __builtin_amdgcn_s_sleep(2);
+        uint32_t ready = load_dev(slot);
+        for (uint32_t spins = 0; ready == 0u && spins < a.spin_limit; ++spins) {
+          __builtin_amdgcn_s_sleep(2);
+          ready = load_dev(slot);
+        }
+        if (ready == 0u) {
+          s_err = 1;
+          raise_error(a.sync, kErrHTimeout);
+        }
       }
       compiler_fence();
 #pragma unroll
@@ -556,7 +591,14 @@ void stream4_kernel(const StreamArgs a) {
     stores_done();
     __syncthreads();
     __shared__ int s_last;
-    if (threadIdx.x == 0) s_last = atomicAdd(a.sync + kSyncTile + tb, 1u) == (uint32_t)(a.splits - 1);
+    if (threadIdx.x == 0) {
+      const uint32_t old = atomicAdd(a.sync + kSyncTile + tb, 1u);
+      if (old >= (uint32_t)a.splits) {  // counters not zero at entry: this block writes the rows as NaN
+        raise_error(a.sync, kErrArrivals);
+        s_err = 1;
+      }
+      s_last = old == (uint32_t)(a.splits - 1) || old >= (uint32_t)a.splits;
+    }
     __syncthreads();
     if (!s_last) return;
     compiler_fence();
@@ -594,7 +636,9 @@ void stream4_kernel(const StreamArgs a) {
     }
   }
 
-  // Epilogue: y = fp16_rn((v + s * H[i, :] . B[n, :]) * gamma[n]) with H, B and gamma from LDS.
+  // Epilogue: y = fp16_rn((v + s * H[i, :] . B[n, :]) * gamma[n]) with H, B and gamma from LDS;
+  // NaN rows when this call or an earlier one on the workspace failed a hand-off.
+  const bool poisoned = err0 != 0u || s_err != 0;
 #pragma unroll
   for (int q = 0; q < kOPT; ++q) {
     const int o = (int)threadIdx.x + 256 * q;
@@ -619,7 +663,7 @@ void stream4_kernel(const StreamArgs a) {
           }
           y = (y + a.scale * ls) * h2f(gs[rr]);
         }
-        a.out[(size_t)i * a.N + n] = f2h_rn(y);
+        a.out[(size_t)i * a.N + n] = poisoned ? kHalfNaN : f2h_rn(y);
       }
     }
   }
@@ -627,7 +671,9 @@ void stream4_kernel(const StreamArgs a) {
     // count this consumer; the slot's last consumer lowers it for the next call
     const int g = tb % slots;
     const uint32_t members = (uint32_t)(a.TB / slots + (g < a.TB % slots ? 1 : 0));
-    if (atomicAdd(slot + 1, 1u) == members - 1u) {
+    const uint32_t old = atomicAdd(slot + 1, 1u);
+    if (old >= members) raise_error(a.sync, kErrArrivals);
+    if (old == members - 1u) {
       store_dev(slot + 1, 0u);
       store_dev(slot, 0u);
     }
@@ -821,7 +867,7 @@ StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank, int ch
   // the block's threads stage the activations with kXR (M > 16: 2 kXR) 16-byte loads each
   const bool staged = (size_t)M * cps * (chunk / 8) <= (size_t)256 * kXR * (M > 16 ? 2 : 1);
   p.ok = M >= 1 && M <= stream_max_m() && (chunk == 512 || chunk == 640) && staged &&
-         (splits == 1 || TB <= (int)(kSyncBytes / 4) - kSyncTile) && fused_rank % 8 == 0 && fused_rank <= kMaxRank;
+         (splits == 1 || TB <= kSyncErrorWord - kSyncTile) && fused_rank % 8 == 0 && fused_rank <= kMaxRank;
   return p;
 }
 
@@ -868,6 +914,8 @@ hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, cons
   a.hpart = reinterpret_cast<float*>(ws + plan.hpart_off);
   a.partial = reinterpret_cast<float*>(ws + plan.partial_off);
   a.sync = sync;
+  a.spin_limit = spin_limit();
+  a.withhold_h = withhold_h() ? 1 : 0;
   const int rows = 16 * plan.tpb;
   const int mb = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : M <= 8 ? 8 : M <= 16 ? 16 : 32;
   const int na = (mb + 15) / 16;

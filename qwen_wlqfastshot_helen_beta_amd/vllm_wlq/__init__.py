@@ -7,7 +7,7 @@ plus trailing defaulted arguments: ``group_size`` (0 = one LUT per row),
 ``lora_A`` (when lora_h / lora_H is None, the op computes the DoRA H itself as
 fp32(fp16(x @ lora_A^T)), the reference caller's F.linear) and ``prepared``
 (the layer's load-time tile-contiguous layout from ``_C.prepare_layer``, used by
-the decode kernel for up to 8 activation rows).
+the decode kernel for up to 32 activation rows).
 Both call the ``_C`` extension, which calls the C ABI of ``libwlq_hip.so``.
 """
 from __future__ import annotations
@@ -94,6 +94,19 @@ def init_workspaces(max_N: int, max_K: int, device: torch.device) -> None:
     _C.init_workspaces(int(max_N), int(max_K), torch.device(device))
 
 
+def check_workspaces(device) -> None:
+    """Raise RuntimeError if a cross-block hand-off failed on a workspace of ``device``
+    (the kernels then wrote the rows concerned, and every later call's rows, as NaN).
+    Waits for the streams that used the workspaces; not for use inside graph capture."""
+    _C.check_workspaces(torch.device(device))
+
+
+def reset_workspaces(device) -> None:
+    """Clear the counter area of every workspace of ``device`` (after check_workspaces
+    raised and the calls that used them have finished)."""
+    _C.reset_workspaces(torch.device(device))
+
+
 def register() -> None:
     """vLLM general-plugin entry point (setup.py:47-51 of the reference); importing
     this package already registered the ops and the quantization config."""
@@ -103,4 +116,5 @@ def register() -> None:
 from .quant_config import WLQFastShotConfig  # noqa: E402
 from .linear_method import WLQLinearMethod  # noqa: E402
 
-__all__ = ["WLQFastShotConfig", "WLQLinearMethod", "init_workspaces", "register"]
+__all__ = ["WLQFastShotConfig", "WLQLinearMethod", "init_workspaces", "check_workspaces", "reset_workspaces",
+           "register"]

@@ -18,6 +18,18 @@ DEV = "cuda"
 # ulps of the reference value (plus a 1e-3*rms floor for values near zero).
 REL_TOL = 2e-3
 
+# Tolerance per config (the same bound everywhere, stated per config as the target asks).
+# "single": against the fp64 oracle that rounds once, as this build does; "reference": also
+# against the reference's own rounding points (M >= 16 rounds x.W0^T to fp16 before the DoRA
+# epilogue rounds again, csrc/vllm_binding.cpp:355-393), which adds up to 0.5 ulp.
+TOLERANCE = {
+    "cfg0": {"rel": REL_TOL, "elementwise": "2^-9 |ref| + 1e-3 rms(ref)", "against": ("single",)},
+    "cfg1": {"rel": REL_TOL, "elementwise": "2^-9 |ref| + 1e-3 rms(ref)", "against": ("single", "reference M>=16")},
+    "cfg2": {"rel": REL_TOL, "elementwise": "2^-9 |ref| + 1e-3 rms(ref)", "against": ("single", "reference")},
+    "cfg3": {"rel": REL_TOL, "elementwise": "2^-9 |ref| + 1e-3 rms(ref)", "against": ("single", "reference M>=16")},
+    "dequant": {"rel": 0.0, "elementwise": "bit-exact", "against": ("oracle dequant",)},
+}
+
 
 def oracle_w0(L: synth.SynthLayer) -> np.ndarray:
     return O.dequant(L.q, L.lut, L.N, L.K, L.bits, L.offsets, L.cols, L.vals, group_size=L.group_size)
@@ -178,3 +190,46 @@ def run_prepared(vw, L: synth.SynthLayer, x: np.ndarray, dora: str = "fused", wi
                                     B, g, L.lora_scale, L.group_size, A, prep)
     torch.cuda.synchronize()
     return out.cpu().numpy(), Hor
+
+
+def rows_subset(L: synth.SynthLayer, rows: np.ndarray):
+    """Bit-exact oracle W0 and the DoRA rows (B, gamma) of the given output rows only:
+    the rows' codes, LUTs and CSR entries are cut out of the layer (offsets rebased), so a
+    full 7B shape is checked at a CPU cost of seconds."""
+    rows = np.asarray(rows)
+    q = L.q.view(np.uint32).reshape(L.N, L.wpr)[rows].ravel()
+    lut = L.lut[rows]
+    offs, cols, vals, base = [], [], [], 0
+    for r in rows:
+        o = L.offsets[r].astype(np.int64)
+        offs.append(o - o[0] + base)
+        cols.append(L.cols[o[0]:o[-1]])
+        vals.append(L.vals[o[0]:o[-1]])
+        base += int(o[-1] - o[0])
+    W0 = O.dequant(q, lut, len(rows), L.K, L.bits, np.stack(offs).astype(np.int32), np.concatenate(cols),
+                   np.concatenate(vals), group_size=L.group_size)
+    B = None if L.B is None else L.B[rows]
+    g = None if L.gamma is None else L.gamma[rows]
+    return W0, B, g
+
+
+def pick_rows(L: synth.SynthLayer, n: int, seed: int, heavy: int = 32) -> np.ndarray:
+    """n random output rows plus the `heavy` rows with the most outliers and the first and
+    last rows (tile and block edges), sorted and unique."""
+    rng = np.random.default_rng(seed)
+    rows = rng.choice(L.N, size=min(n, L.N), replace=False)
+    dens = np.argsort(np.diff(L.offsets[:, [0, -1]], axis=1).ravel())[-heavy:]
+    return np.unique(np.concatenate([rows, dens, [0, L.N - 1]]))
+
+
+def check_rows(y_rows: np.ndarray, x_rows: np.ndarray, L: synth.SynthLayer, rows: np.ndarray, H_rows, what: str,
+               reference_rounding: bool):
+    """Compare output rows `rows` of y (already sliced: [len(x_rows), len(rows)]) with the
+    oracle: single rounding always, the reference's double rounding too when asked."""
+    W0, B, g = rows_subset(L, rows)
+    ref = O.linear_forward(x_rows, W0, H_rows, B, g, L.lora_scale, round_gemm_output=False)
+    err = check_close(y_rows, ref, what=what)
+    if reference_rounding:
+        ref2 = O.linear_forward(x_rows, W0, H_rows, B, g, L.lora_scale, round_gemm_output=True)
+        check_close(y_rows, ref2, what=what + " (reference rounding)")
+    return err

@@ -2,14 +2,14 @@
 outlier density 0.1-2% with 20% heavy rows holding 10x the mean, DoRA rank 0/8/16/64,
 LUT groups 64 and 128, 4-bit and 3-bit, M = 1, 4 and 512.  The oracle checks a
 random subset of output rows (sliced out of the layer with their CSR entries), which
-keeps the CPU side to seconds at the full shape."""
+keeps the CPU side to seconds at the full shape.  Each case runs both the row-aligned
+kernel and the prepared-layout path that a loaded layer uses."""
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from gpu_helpers import check_close, run_product
-from oracle import wlq_oracle as O
+from gpu_helpers import check_rows, pick_rows, run_prepared, run_product
 from qwen_wlqfastshot_helen_beta_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -21,34 +21,15 @@ def _case(msg):
     print(f"[case] {msg}", flush=True)
 
 
-def rows_subset(L: synth.SynthLayer, rows: np.ndarray):
-    """W0 (bit-exact oracle dequant) and DoRA rows for the given output rows."""
-    q = L.q.view(np.uint32).reshape(L.N, L.wpr)[rows].ravel()
-    lut = L.lut[rows]
-    offs, cols, vals, base = [], [], [], 0
-    for r in rows:
-        o = L.offsets[r].astype(np.int64)
-        offs.append(o - o[0] + base)
-        cols.append(L.cols[o[0]:o[-1]])
-        vals.append(L.vals[o[0]:o[-1]])
-        base += int(o[-1] - o[0])
-    W0 = O.dequant(q, lut, len(rows), L.K, L.bits, np.stack(offs).astype(np.int32), np.concatenate(cols),
-                   np.concatenate(vals), group_size=L.group_size)
-    B = None if L.B is None else L.B[rows]
-    g = None if L.gamma is None else L.gamma[rows]
-    return W0, B, g
-
-
 def _check(vw, L, M, seed, what):
-    rng = np.random.default_rng(seed)
+    """Row-layout kernel (no prepared buffer) and the prepared path apply() uses, both
+    against the oracle on a row subset that includes the densest (heavy) rows."""
     x = synth.make_activations(M, L.K, seed=seed)
+    rows = pick_rows(L, 192, seed=seed, heavy=64)
     y, H = run_product(vw, L, x, fused_h=L.B is not None)
-    rows = np.sort(rng.choice(L.N, size=192, replace=False))
-    heavy = np.argsort(np.diff(L.offsets[:, [0, -1]], axis=1).ravel())[-64:]  # the densest rows too
-    rows = np.unique(np.concatenate([rows, heavy]))
-    W0, B, g = rows_subset(L, rows)
-    ref = O.linear_forward(x, W0, H, B, g, L.lora_scale, round_gemm_output=False)
-    check_close(y[:, rows], ref, what=what)
+    check_rows(y[:, rows], x, L, rows, H, what=what + " row layout", reference_rounding=M >= 16)
+    yp, Hp = run_prepared(vw, L, x, dora="fused" if L.B is not None else "none")
+    check_rows(yp[:, rows], x, L, rows, Hp, what=what + " prepared", reference_rounding=M >= 16)
 
 
 @pytest.mark.parametrize("density", [0.001, 0.005, 0.01, 0.02])

@@ -107,8 +107,19 @@ def test_abi_exports_every_declared_symbol():
     assert len(names) >= 12
     for n in names:
         assert hasattr(lib, n), f"libwlq_hip.so does not export {n}"
-    assert lib.wlq_abi_version() == 4
+    assert lib.wlq_abi_version() == 5
     assert lib.wlq_status_string(4) == b"WLQ_ERR_CAPACITY" or b"capacity" in lib.wlq_status_string(4).lower()
+
+
+def test_abi_workspace_status_without_counter_area():
+    """Host-side argument handling of the workspace status/reset entry points (no GPU call):
+    a null workspace or one below the 16 KiB counter area has no counters to check."""
+    lib = load_abi()
+    assert lib.wlq_workspace_status(None, 0, None) == 0
+    assert lib.wlq_workspace_status(None, 1 << 20, None) == 0
+    assert lib.wlq_workspace_reset(None, 1 << 20, None) == 1  # WLQ_ERR_NULL_POINTER
+    assert b"non-null" in lib.wlq_last_error()
+    assert b"hand-off" in lib.wlq_status_string(7)
 
 
 def test_abi_prepared_bytes():
