@@ -297,10 +297,8 @@ void stream4_kernel(const StreamArgs a) {
   uint16_t* bs = reinterpret_cast<uint16_t*>(red + 4 * NA * 256);
   uint16_t* gs = bs + ROWS * a.r;
 
-  // Sticky error of an earlier call (loaded now, used by the epilogue) and this call's own.
+  // This call's own hand-off failure (set by the H wait or an arrival count).
   __shared__ int s_err;
-  uint32_t err0 = 0;
-  if (a.sync != nullptr) err0 = load_dev(a.sync + kSyncErr);
   if (threadIdx.x == 0) s_err = 0;
 
   // Outlier pass mapping: thread (rho, j) walks entries j, j + TPR, ... of block row rho.
@@ -370,6 +368,11 @@ void stream4_kernel(const StreamArgs a) {
   Slab buf[kPF];
 #pragma unroll
   for (int u = 0; u < kPF; ++u) load_slab(buf[u], min(s0 + ph + WPT * u, s_last));
+  // Sticky error word of an earlier call (used by the epilogue): a plain load, served by L2
+  // after the XCD's first block (a kernel starts with invalidated caches, so earlier calls'
+  // bits are seen), issued behind the slab prefetch so the first slab does not wait for it.
+  compiler_fence();
+  const uint32_t err0 = a.sync != nullptr ? a.sync[kSyncErr] : 0u;
 
 #pragma unroll
   for (int k = 0; k < XR; ++k) {
