@@ -161,6 +161,26 @@ int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c,
                       const void* lora_B, const void* dora_gamma, const void* lora_A, float lora_scale, int32_t r,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* wlq_gemm_prepared without a workspace argument, for callers that cannot allocate
+ * device memory (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): it allocates nothing and calls no allocating routine.  No counterpart in
+ * the reference.  Its kernels use the library's own scratch instead: a 16 MiB device
+ * array per GPU (a file-scope __device__ array, held until the process ends), counter
+ * area first.  A call whose decode plan needs more than that (e.g. the 37888-row
+ * gate_up projection at M >= 16, whose K splits write fp32 partials of M * N * splits)
+ * returns WLQ_ERR_CAPACITY without launching anything; M > 32 runs the GEMM with the
+ * split count the scratch allows.  Every call on a GPU shares that GPU's scratch: calls
+ * that overlap in time on one GPU (different streams, or threads without ordering) race
+ * and must not be issued.  The scratch's counters are left zero by every call; a failed
+ * hand-off (see the workspace notes above) leaves this GPU's scratch poisoned (NaN rows)
+ * for the rest of the process. */
+int wlq_gemm_prepared_noalloc(const void* X, const int32_t* q_packed, const void* lut_c, const void* prepared,
+                              size_t prepared_bytes, void* out, int64_t M, int64_t N, int64_t K, int32_t bits,
+                              int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets,
+                              const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz,
+                              const float* lora_H, const void* lora_B, const void* dora_gamma, const void* lora_A,
+                              float lora_scale, int32_t r, hipStream_t stream);
+
 /* Bit-exact W_out[N, K] (fp16) = lut[n, g(k), code(n, k)], outliers overwritten with e5m2 << 8.
  * Replaces launch_dequant_patch_metalog (csrc/gemm_kernel.cu:475-503, declared
  * csrc/vllm_binding.cpp:54-68). */

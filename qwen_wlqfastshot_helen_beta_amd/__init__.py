@@ -55,6 +55,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         "wlq_prepare": (ctypes.c_int, [vp, vp, c_i64, c_i64, c_i32, c_i32, vp, vp, vp, c_i64, vp, c_sz, vp]),
         "wlq_gemm_prepared": (ctypes.c_int, [vp, vp, vp, vp, c_sz, vp, c_i64, c_i64, c_i64, c_i32, c_i64, c_i32, vp,
                                              vp, vp, c_i64, vp, vp, vp, vp, c_f, c_i32, vp, c_sz, vp]),
+        "wlq_gemm_prepared_noalloc": (ctypes.c_int, [vp, vp, vp, vp, c_sz, vp, c_i64, c_i64, c_i64, c_i32, c_i64,
+                                                     c_i32, vp, vp, vp, c_i64, vp, vp, vp, vp, c_f, c_i32, vp]),
         "wlq_dequant": (ctypes.c_int, [vp, vp, vp, c_i64, c_i64, c_i32, c_i64, c_i32, vp, vp, vp, vp]),
         "wlq_dora_epilogue": (ctypes.c_int, [vp, vp, vp, vp, c_f, c_i32, c_i64, c_i64, vp]),
         "wlq_workspace_status": (ctypes.c_int, [vp, c_sz, vp]),

@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 
 #include "wlq_abi.h"
 #include "wlq_internal.h"
@@ -225,6 +226,109 @@ int run_product(const wlq::Layer& L, wlq::Dora D, const void* X, void* out, int6
   return hip_status(wlq::launch_gemm(L, D, x, y, (int)M, p, w, stream), fn);
 }
 
+// wlq_gemm_prepared with a workspace of the caller's (strict = false: a stream-kernel plan
+// whose workspace does not fit falls back to the row-layout kernels, which adapt their
+// splits) or the library's scratch (strict = true: such a call is refused instead).
+int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c, const void* prepared,
+                       size_t prepared_bytes, void* out, int64_t M, int64_t N, int64_t K, int32_t bits,
+                       int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets,
+                       const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz, const float* lora_H,
+                       const void* lora_B, const void* dora_gamma, const void* lora_A, float lora_scale, int32_t r,
+                       void* workspace, size_t workspace_bytes, hipStream_t stream, const char* fn, bool strict) {
+  wlq::Layer L{};
+  int st = make_layer(q_packed, lut_c, N, K, bits, words_per_row, group_size, chunk_offsets, chunk_cols, chunk_vals,
+                      fn, &L);
+  if (st != WLQ_OK) return st;
+  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_A, lora_scale, r);
+  if (prepared != nullptr && M >= 1 && M <= wlq::stream_max_m() && L.N > 0 && X != nullptr && out != nullptr &&
+      wlq::prepared_supported(L.N, L.K, L.bits, L.group_size) && nnz >= 0 && (L.offsets != nullptr || nnz == 0)) {
+    const size_t need = wlq::prepared_layout(L.N, L.K, L.group_size, nnz).bytes;
+    if (prepared_bytes < need) {
+      wlq::set_error("%s: the prepared buffer holds %zu bytes, the layer needs %zu (nnz=%lld)", fn, prepared_bytes,
+                     need, (long long)nnz);
+      return WLQ_ERR_CAPACITY;
+    }
+    const bool fused_h = D.r > 0 && D.H == nullptr;
+    // the kernel stages B rows with 16-byte loads (r % 8 == 0) and x / lora_A rows likewise
+    const bool dora_ok = D.r == 0 || (D.r % 8 == 0 && D.r <= wlq::stream_max_rank() &&
+                                      (reinterpret_cast<uintptr_t>(D.B) & 15u) == 0);
+    const bool aligned = (reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (reinterpret_cast<uintptr_t>(prepared) & 255u) == 0 &&
+                         (!fused_h || (reinterpret_cast<uintptr_t>(D.A) & 15u) == 0) && dora_ok;
+    const wlq::StreamPlan p =
+        wlq::plan_stream(L.N, L.K, (int)M, current_cu_count(), fused_h ? D.r : 0, L.chunk);
+    const bool need_sync = p.splits > 1 || fused_h;
+    const size_t ws = workspace != nullptr ? workspace_bytes : 0;
+    const bool ws_ok = !need_sync || ws >= wlq::kSyncBytes + p.workspace_bytes;
+    const bool runs = p.ok && aligned && (!fused_h || D.r <= wlq::stream_max_rank());
+    if (runs && !ws_ok && strict) {
+      wlq::set_error("%s: M=%lld N=%lld K=%lld needs %zu bytes of scratch, more than the %zu bytes it holds", fn,
+                     (long long)M, (long long)N, (long long)K, wlq::kSyncBytes + p.workspace_bytes, ws);
+      return WLQ_ERR_CAPACITY;
+    }
+    if (runs && ws_ok) {
+      char* wbase = reinterpret_cast<char*>(workspace);
+      uint32_t* sync = need_sync ? reinterpret_cast<uint32_t*>(wbase) : nullptr;
+      float* w = need_sync ? reinterpret_cast<float*>(wbase + wlq::kSyncBytes) : nullptr;
+      return hip_status(wlq::launch_stream(L, prepared, nnz, D, reinterpret_cast<const uint16_t*>(X),
+                                           reinterpret_cast<uint16_t*>(out), (int)M, p, w, sync, stream),
+                        fn);
+    }
+  }
+  return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, fn);
+}
+
+// ------------------------------------------------------------ no-allocation scratch
+// Device memory of wlq_gemm_prepared_noalloc: one array per GPU (each device that loads
+// the library holds its own copy until the process ends), in the same layout as a
+// caller's workspace: the 16 KiB counter area, then split partials and DoRA H sums.
+// On the host, `scratch` only names the symbol; its device address comes from
+// hipGetSymbolAddress, once per device with that device current, and only that address
+// is passed to kernels and fills.
+constexpr size_t kScratchBytes = (size_t)16 << 20;  // 16 MiB
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The current device's scratch address; the first call on a device looks it up and
+// clears the counter area on `stream` (the array is zero at load; the clear also holds
+// when the library is loaded into a process that ran other code on the device).  Under
+// graph capture the clear is recorded instead, and no clear is needed: the array is
+// still as the loader left it, zero.
+int scratch_for_current_device(hipStream_t stream, void** out_ptr) {
+  int dev = 0;
+  int st = hip_status(hipGetDevice(&dev), "wlq_gemm_prepared_noalloc");
+  if (st != WLQ_OK) return st;
+  if (dev < 0 || dev >= kMaxDevices) {
+    wlq::set_error("wlq_gemm_prepared_noalloc: device %d is beyond the %d the library serves", dev, kMaxDevices);
+    return WLQ_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    st = hip_status(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "wlq_gemm_prepared_noalloc: hipGetSymbolAddress");
+    if (st != WLQ_OK) return st;
+    if (ptr == nullptr) {
+      wlq::set_error("wlq_gemm_prepared_noalloc: hipGetSymbolAddress returned a null scratch address");
+      return WLQ_ERR_HIP;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+      (void)hipGetLastError();
+      cs = hipStreamCaptureStatusNone;
+    }
+    if (cs == hipStreamCaptureStatusNone) {
+      hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)(wlq::kSyncWords + 255) / 256), dim3(256), 0, stream,
+                         reinterpret_cast<uint32_t*>(ptr), wlq::kSyncWords);
+      st = hip_status(hipGetLastError(), "wlq_gemm_prepared_noalloc: clearing the scratch counters");
+      if (st != WLQ_OK) return st;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out_ptr = g_scratch_ptr[dev];
+  return WLQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -323,40 +427,23 @@ int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c,
                       const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz, const float* lora_H,
                       const void* lora_B, const void* dora_gamma, const void* lora_A, float lora_scale, int32_t r,
                       void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  wlq::Layer L{};
-  int st = make_layer(q_packed, lut_c, N, K, bits, words_per_row, group_size, chunk_offsets, chunk_cols, chunk_vals,
-                      "wlq_gemm_prepared", &L);
+  return gemm_prepared_impl(X, q_packed, lut_c, prepared, prepared_bytes, out, M, N, K, bits, words_per_row,
+                            group_size, chunk_offsets, chunk_cols, chunk_vals, nnz, lora_H, lora_B, dora_gamma, lora_A,
+                            lora_scale, r, workspace, workspace_bytes, stream, "wlq_gemm_prepared", false);
+}
+
+int wlq_gemm_prepared_noalloc(const void* X, const int32_t* q_packed, const void* lut_c, const void* prepared,
+                              size_t prepared_bytes, void* out, int64_t M, int64_t N, int64_t K, int32_t bits,
+                              int64_t words_per_row, int32_t group_size, const int32_t* chunk_offsets,
+                              const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz,
+                              const float* lora_H, const void* lora_B, const void* dora_gamma, const void* lora_A,
+                              float lora_scale, int32_t r, hipStream_t stream) {
+  void* ws = nullptr;
+  const int st = scratch_for_current_device(stream, &ws);
   if (st != WLQ_OK) return st;
-  const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_A, lora_scale, r);
-  if (prepared != nullptr && M >= 1 && M <= wlq::stream_max_m() && L.N > 0 && X != nullptr && out != nullptr &&
-      wlq::prepared_supported(L.N, L.K, L.bits, L.group_size) && nnz >= 0 && (L.offsets != nullptr || nnz == 0)) {
-    const size_t need = wlq::prepared_layout(L.N, L.K, L.group_size, nnz).bytes;
-    if (prepared_bytes < need) {
-      wlq::set_error("wlq_gemm_prepared: the prepared buffer holds %zu bytes, the layer needs %zu (nnz=%lld)",
-                     prepared_bytes, need, (long long)nnz);
-      return WLQ_ERR_CAPACITY;
-    }
-    const bool fused_h = D.r > 0 && D.H == nullptr;
-    // the kernel stages B rows with 16-byte loads (r % 8 == 0) and x / lora_A rows likewise
-    const bool dora_ok = D.r == 0 || (D.r % 8 == 0 && D.r <= wlq::stream_max_rank() &&
-                                      (reinterpret_cast<uintptr_t>(D.B) & 15u) == 0);
-    const bool aligned = (reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (reinterpret_cast<uintptr_t>(prepared) & 255u) == 0 &&
-                         (!fused_h || (reinterpret_cast<uintptr_t>(D.A) & 15u) == 0) && dora_ok;
-    const wlq::StreamPlan p =
-        wlq::plan_stream(L.N, L.K, (int)M, current_cu_count(), fused_h ? D.r : 0, L.chunk);
-    const bool need_sync = p.splits > 1 || fused_h;
-    const size_t ws = workspace != nullptr ? workspace_bytes : 0;
-    const bool ws_ok = !need_sync || ws >= wlq::kSyncBytes + p.workspace_bytes;
-    if (p.ok && aligned && ws_ok && (!fused_h || D.r <= wlq::stream_max_rank())) {
-      char* wbase = reinterpret_cast<char*>(workspace);
-      uint32_t* sync = need_sync ? reinterpret_cast<uint32_t*>(wbase) : nullptr;
-      float* w = need_sync ? reinterpret_cast<float*>(wbase + wlq::kSyncBytes) : nullptr;
-      return hip_status(wlq::launch_stream(L, prepared, nnz, D, reinterpret_cast<const uint16_t*>(X),
-                                           reinterpret_cast<uint16_t*>(out), (int)M, p, w, sync, stream),
-                        "wlq_gemm_prepared");
-    }
-  }
-  return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, "wlq_gemm_prepared");
+  return gemm_prepared_impl(X, q_packed, lut_c, prepared, prepared_bytes, out, M, N, K, bits, words_per_row,
+                            group_size, chunk_offsets, chunk_cols, chunk_vals, nnz, lora_H, lora_B, dora_gamma, lora_A,
+                            lora_scale, r, ws, kScratchBytes, stream, "wlq_gemm_prepared_noalloc", true);
 }
 
 int wlq_workspace_status(const void* workspace, size_t workspace_bytes, hipStream_t stream) {
