@@ -135,6 +135,31 @@ __device__ __forceinline__ void dequant_word4(uint32_t w, const LutPlanes<4>& t,
   interleave(lo, ho, out[2], out[3]);
 }
 
+// Prepared ("selector-ready") 4-bit encoding of 8 codes c0..c7 (columns 0..7) in one word,
+// used by the prepared layout of the decode kernel.  Byte j (j = 0..3) holds
+//   bits 0-2: c_j & 7        bit 7: c_j >> 3                    (the "A" codes, columns 0-3)
+//   bits 4-6: c_{4+j} & 7    bit 3: c_{4+((j+3)&3)} >> 3        (the "B" codes, columns 4-7)
+// so  w & 0x87878787  is the lower-table selector of the A codes (c or 0x80|c, >= 13 -> 0xFF)
+// and, after a 4-bit rotate right (each byte's high nibble moves down and the next byte's
+// low nibble moves up, bringing the B code's top bit to bit 7), the same mask gives the B
+// selectors.  XOR 0x80 turns a lower-table selector into the upper-table one.  Per 8
+// codes: 5 selector ops, 8 perms + 4 ANDs for the two planes, 4 perms to interleave.
+__host__ __device__ constexpr uint32_t sel_encode_byte(const uint32_t c[8], int j) {
+  return (c[j] & 7u) | ((c[j] >> 3) << 7) | ((c[4 + j] & 7u) << 4) | ((c[4 + ((j + 3) & 3)] >> 3) << 3);
+}
+
+// One selector-encoded word -> 4 fp16 pairs in natural column order (0,1), (2,3), (4,5), (6,7).
+__device__ __forceinline__ void dequant_word4s(uint32_t w, const LutPlanes<4>& t, uint32_t out[4]) {
+  const uint32_t sa = w & 0x87878787u;
+  const uint32_t rb = __builtin_amdgcn_alignbit(w, w, 4);  // rotate right by 4
+  const uint32_t sb = rb & 0x87878787u;
+  uint32_t la, ha, lb, hb;
+  lookup16(t, sa, sa ^ 0x80808080u, la, ha);
+  lookup16(t, sb, sb ^ 0x80808080u, lb, hb);
+  interleave(la, ha, out[0], out[1]);
+  interleave(lb, hb, out[2], out[3]);
+}
+
 // <= 8 entries: selector bytes are the codes themselves.
 template <int BITS>
 __device__ __forceinline__ void dequant_sel8(uint32_t se, uint32_t so, const LutPlanes<BITS>& t, uint32_t out[4]) {

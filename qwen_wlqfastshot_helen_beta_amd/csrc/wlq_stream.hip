@@ -15,10 +15,11 @@
 // Prepared layout (built once per layer by the prepare kernels below, from the
 // reference's row-aligned codes, LUTs and chunk CSR):
 //   codes  u32x4 [T][S][64]     T = ceil(N/16) row tiles, S = ceil(K/128) slabs;
-//                               lane l = r + 16*kq holds the 32 nibble codes of row
-//                               16t + r, columns 128s + 32kq .. +31 (4 words), so
-//                               one wave load is 1 KB contiguous and lands in the
-//                               MFMA B-operand lane order.
+//                               lane l = r + 16*kq holds the 32 codes of row 16t + r,
+//                               columns 128s + 32kq .. +31 (4 words, 8 columns each in
+//                               the selector-ready encoding of wlq_device.h), so one
+//                               wave load is 1 KB contiguous and lands in the MFMA
+//                               B-operand lane order.
 //   planes u32x4 [T][ng][2][16] the low and the high bytes of the 16 fp16 LUT
 //                               entries of row 16t + r, group g (the V_PERM_B32
 //                               byte planes, wlq_device.h).
@@ -297,7 +298,10 @@ void stream4_kernel(const StreamArgs a) {
   uint16_t* bs = reinterpret_cast<uint16_t*>(red + 4 * NA * 256);
   uint16_t* gs = bs + ROWS * a.r;
 
-  // This call's own hand-off failure (set by the H wait or an arrival count).
+  // Poison flag: this call's own hand-off failure (an H wait that ran out, an arrival count
+  // beyond one call's) or the workspace's sticky error word, which a block reads together with
+  // its first cross-block load (H or the split partials), so the read adds no round trip.
+  // Blocks that hand nothing over have no counters that could be stale.
   __shared__ int s_err;
   if (threadIdx.x == 0) s_err = 0;
 
@@ -368,11 +372,6 @@ void stream4_kernel(const StreamArgs a) {
   Slab buf[kPF];
 #pragma unroll
   for (int u = 0; u < kPF; ++u) load_slab(buf[u], min(s0 + ph + WPT * u, s_last));
-  // Sticky error word of an earlier call (used by the epilogue): a plain load, served by L2
-  // after the XCD's first block (a kernel starts with invalidated caches, so earlier calls'
-  // bits are seen), issued behind the slab prefetch so the first slab does not wait for it.
-  compiler_fence();
-  const uint32_t err0 = a.sync != nullptr ? a.sync[kSyncErr] : 0u;
 
 #pragma unroll
   for (int k = 0; k < XR; ++k) {
@@ -381,8 +380,7 @@ void stream4_kernel(const StreamArgs a) {
       const int i = u / upr;
       const int c8 = u - i * upr;
       const bool inside = s0 * 128 + (c8 << 3) < a.K;  // K % 8 == 0
-      *reinterpret_cast<u32x4_t*>(xs + i * a.xstride + (c8 << 3)) =
-          inside ? permute_p(xv[k]) : u32x4_t{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4_t*>(xs + i * a.xstride + (c8 << 3)) = inside ? xv[k] : u32x4_t{0u, 0u, 0u, 0u};
     }
   }
   if (threadIdx.x < 16) reinterpret_cast<uint32_t*>(zline)[threadIdx.x] = 0u;
@@ -429,7 +427,7 @@ void stream4_kernel(const StreamArgs a) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       uint32_t b[4];
-      dequant_word4(w[q], t4, b);
+      dequant_word4s(w[q], t4, b);
       const u32x4_t bv = {b[0], b[1], b[2], b[3]};
       const u32x4_t av = *reinterpret_cast<const u32x4_t*>(xp + (xrow ? 8 * q : 0));
       acc[0] = mfma16x16x32(av, bv, acc[0]);
@@ -481,7 +479,11 @@ void stream4_kernel(const StreamArgs a) {
   uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
   constexpr int kHB = (MB * kMaxRank + 255) / 256;  // H words per thread (M * r <= MB * 64)
   float hv[kHB];
+  // Only the threads that own H elements load them (the others return; store_h and the
+  // epilogue go through LDS after a barrier).  Thread 0 also reads the workspace's sticky
+  // error word, in parallel with H (no extra round trip).
   auto load_h = [&]() __attribute__((always_inline)) {
+    if ((int)threadIdx.x >= a.M * a.r) return;
     if (a.h_blocks > 0) {
       if (lane == 0) {
         uint32_t ready = load_dev(slot);
@@ -495,8 +497,11 @@ void stream4_kernel(const StreamArgs a) {
         }
       }
       compiler_fence();
+      uint32_t err = 0u;
+      if (threadIdx.x == 0) err = load_dev(a.sync + kSyncErr);
 #pragma unroll
       for (int u = 0; u < kHB; ++u) hv[u] = load_dev(a.hfin + min((int)threadIdx.x + 256 * u, a.M * a.r - 1));
+      if (err != 0u) s_err = 1;
     } else {
 #pragma unroll
       for (int u = 0; u < kHB; ++u) hv[u] = a.H[min((int)threadIdx.x + 256 * u, a.M * a.r - 1)];
@@ -518,7 +523,7 @@ void stream4_kernel(const StreamArgs a) {
     const int xc0 = s0 * 128;
     auto entry = [&](uint32_t col, float d) __attribute__((always_inline)) {
       const int xc = (int)col - xc0;
-      const int xi = (xc & ~7) + p_slot(xc & 7);
+      const int xi = xc;  // activations are staged in natural column order
 #pragma unroll
       for (int i = 0; i < MB; ++i)
         if (i < a.M) corr[i] += d * h2f(xs[i * a.xstride + xi]);
@@ -605,6 +610,9 @@ void stream4_kernel(const StreamArgs a) {
     __syncthreads();
     if (!s_last) return;
     compiler_fence();
+    // the sticky error word, read together with the partials
+    uint32_t err = 0u;
+    if (threadIdx.x == 0) err = load_dev(a.sync + kSyncErr);
     // Sum the split partials in split order, kSumBatch splits of every output in flight at once
     // (clamped addresses; the sums take only splits < a.splits).
     constexpr int kSumBatch = 8;
@@ -631,17 +639,20 @@ void stream4_kernel(const StreamArgs a) {
         for (int u = 0; u < kSumBatch; ++u)
           if (sp0 + u < a.splits) v[q] += t[q][u];
     }
-    if (threadIdx.x == 0) store_dev(a.sync + kSyncTile + tb, 0u);
+    if (threadIdx.x == 0) {
+      store_dev(a.sync + kSyncTile + tb, 0u);
+      if (err != 0u) s_err = 1;
+    }
     if (a.r > 0 && !h_early) {  // the last split block: computed H now
       load_h();
       store_h();
-      __syncthreads();
     }
+    __syncthreads();
   }
 
   // Epilogue: y = fp16_rn((v + s * H[i, :] . B[n, :]) * gamma[n]) with H, B and gamma from LDS;
   // NaN rows when this call or an earlier one on the workspace failed a hand-off.
-  const bool poisoned = err0 != 0u || s_err != 0;
+  const bool poisoned = s_err != 0;
 #pragma unroll
   for (int q = 0; q < kOPT; ++q) {
     const int o = (int)threadIdx.x + 256 * q;
@@ -685,8 +696,9 @@ void stream4_kernel(const StreamArgs a) {
 
 // ---------------------------------------------------------------- preparation
 
-// 4-bit rows are copied word for word; 3-bit rows (ten codes per word, bits 3c..3c+2)
-// are rewritten as eight nibble codes per word, columns >= K as code 0.
+// Every word holds the 8 codes of 8 consecutive columns in the selector-ready encoding of
+// wlq_device.h (sel_encode_byte); 4-bit codes come from the row-aligned words (code c at
+// bits 4c), 3-bit codes from the ten-per-word layout (values 0..7), columns >= K as code 0.
 __global__ __launch_bounds__(256) void prep_codes_kernel(const uint32_t* __restrict__ q, int N, int K, int wpr,
                                                          int bits, int T, int S, u32x4_t* __restrict__ codes) {
   const size_t total = (size_t)T * S * 64;
@@ -697,24 +709,23 @@ __global__ __launch_bounds__(256) void prep_codes_kernel(const uint32_t* __restr
     const int t = (int)(ts / (size_t)S);
     const int n = 16 * t + (l & 15);
     const int w0 = 16 * s + 4 * (l >> 4);
-    u32x4_t v = {0u, 0u, 0u, 0u};
-    if (bits == 4) {
-      if (n < N && w0 + 4 <= wpr) v = *reinterpret_cast<const u32x4_t*>(q + (size_t)n * wpr + w0);
-    } else if (n < N) {
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (n < N) {
       const uint32_t* qrow = q + (size_t)n * wpr;
-      uint32_t w[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        uint32_t word = 0u;
-        for (int c = 0; c < 8; ++c) {
-          const int col = 8 * (w0 + j) + c;
-          if (col < K) word |= ((qrow[col / 10] >> (3 * (col % 10))) & 7u) << (4 * c);
+        uint32_t c[8];
+        for (int i = 0; i < 8; ++i) {
+          const int col = 8 * (w0 + j) + i;
+          uint32_t code = 0u;
+          if (col < K) code = bits == 4 ? (qrow[col >> 3] >> (4 * (col & 7))) & 15u : (qrow[col / 10] >> (3 * (col % 10))) & 7u;
+          c[i] = code;
         }
-        w[j] = word;
+        w[j] = sel_encode_byte(c, 0) | (sel_encode_byte(c, 1) << 8) | (sel_encode_byte(c, 2) << 16) |
+               (sel_encode_byte(c, 3) << 24);
       }
-      v = u32x4_t{w[0], w[1], w[2], w[3]};
     }
-    codes[idx] = v;
+    codes[idx] = u32x4_t{w[0], w[1], w[2], w[3]};
   }
 }
 

@@ -108,25 +108,31 @@ def oracle_product(L: synth.SynthLayer, x: np.ndarray, H, with_csr: bool = True,
     return O.linear_forward(x, W0, H, L.B, L.gamma, L.lora_scale, round_gemm_output=round_gemm_output)
 
 
+def selector_encode(c8: np.ndarray) -> np.ndarray:
+    """Codes [..., 8] (columns 0..7 of a word, values < 16) -> the prepared layout's words:
+    byte j = (c_j & 7) | (c_j >> 3) << 7 | (c_{4+j} & 7) << 4 | (c_{4+(j+3)%4} >> 3) << 3."""
+    c8 = c8.astype(np.uint32)
+    a, b = c8[..., 0:4], c8[..., 4:8]
+    bprev = b[..., [3, 0, 1, 2]]
+    byte = (a & 7) | ((a >> 3) << 7) | ((b & 7) << 4) | ((bprev >> 3) << 3)
+    return byte[..., 0] | (byte[..., 1] << 8) | (byte[..., 2] << 16) | (byte[..., 3] << 24)
+
+
 def prepared_reference(L: synth.SynthLayer):
     """numpy rebuild of the prepared (tile-contiguous) layout from the reference-format
     arrays: (codes u32 [T, S, 64, 4], planes u8 [T, ng, 2, 16, 16], gcol, delta).
     Codes: lane l = r + 16 kq of tile t, slab s holds words 16 s + 4 kq .. +3 of row
-    16 t + r (4-bit: the row-aligned words as they are; 3-bit: the codes re-packed
-    eight 4-bit nibbles per word, columns >= K zero); planes: low / high bytes of the
+    16 t + r, each the 8 codes of 8 columns in the selector-ready encoding
+    (selector_encode; columns >= K as code 0); planes: low / high bytes of the
     16 LUT entries of row 16 t + r, group g (3-bit: 8 entries, then zeros);
     gcol / delta: the oracle's outlier_delta."""
     N, K = L.N, L.K
     T, S = -(-N // 16), -(-K // 128)
     ng = 1 if L.group_size <= 0 or L.group_size >= K else -(-K // L.group_size)
     qpad = np.zeros((T * 16, S * 16), dtype=np.uint32)
-    if L.bits == 4:
-        qpad[:N, :L.wpr] = L.q.view(np.uint32).reshape(N, L.wpr)
-    else:
-        c = np.zeros((N, S * 128), dtype=np.uint32)
-        c[:, :K] = O.unpack_row_aligned(L.q, N, K, L.bits)
-        nib = c.reshape(N, S * 16, 8) << (4 * np.arange(8, dtype=np.uint32))
-        qpad[:N] = np.bitwise_or.reduce(nib, axis=2)
+    c = np.zeros((N, S * 128), dtype=np.uint32)
+    c[:, :K] = O.unpack_row_aligned(L.q, N, K, L.bits)
+    qpad[:N] = selector_encode(c.reshape(N, S * 16, 8))
     codes = qpad.reshape(T, 16, S, 4, 4).transpose(0, 2, 3, 1, 4).reshape(T, S, 64, 4)
     nl = 1 << L.bits
     lpad = np.zeros((T * 16, ng, 16), dtype=np.uint16)
