@@ -437,6 +437,89 @@ void stream4_kernel(const StreamArgs a) {
       }
     }
   };
+  // DoRA H into registers, by the threads that own H elements.  A caller's H is loaded
+  // directly.  The computed H needs the block's ready slot (raised by the DoRA finisher,
+  // normally long before the tile blocks end): lane 0 of each owner wave polls it (after
+  // spin_limit polls the wait gives up, raises kErrHTimeout and the block writes NaN rows
+  // rather than hang), then the owners load H.  One K split: every tile block loads H after its
+  // slab loop, so the loads overlap the outlier pass; several: only the block that finishes the
+  // rows does.  A block counts itself on the slot after all its polls (a barrier) and the slot's
+  // last consumer lowers it, so no slot is lowered while one of its tile blocks still polls.
+  const int slots = min(a.TB, kMaxSlots);
+  uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
+  constexpr int kHB = (MB * kMaxRank + 255) / 256;  // H words per thread (M * r <= MB * 64)
+  float hv[kHB];
+  bool h_have = false;               // this thread's H words are in hv
+  const bool h_owner = (int)threadIdx.x < a.M * a.r;
+  const bool h_fused = a.r > 0 && a.h_blocks > 0;
+  // H words of an owner thread once the slot is known raised; thread 0 also reads the
+  // workspace's sticky error word, in parallel with H (no extra round trip).
+  auto fetch_h = [&]() __attribute__((always_inline)) {
+    uint32_t err = 0u;
+    if (threadIdx.x == 0) err = load_dev(a.sync + kSyncErr);
+    // H is read through the caches: no block touches hfin before it saw the slot raised, and a
+    // kernel starts with invalidated caches, so the first read of the line on each XCD brings
+    // the published values and later blocks on that XCD hit its L2.
+    const float* hf = a.hfin;
+#pragma unroll
+    for (int u = 0; u < kHB; ++u) hv[u] = hf[min((int)threadIdx.x + 256 * u, a.M * a.r - 1)];
+    if (err != 0u) s_err = 1;
+    h_have = true;
+  };
+  // Blocking: only the threads that own H elements load them (store_h and the epilogue go
+  // through LDS after a barrier).
+  auto load_h = [&]() __attribute__((always_inline)) {
+    if (!h_owner || h_have) return;
+    if (a.h_blocks > 0) {
+      if (lane == 0) {
+        uint32_t ready = load_dev(slot);
+        for (uint32_t spins = 0; ready == 0u && spins < a.spin_limit; ++spins) {
+          __builtin_amdgcn_s_sleep(2);
+          ready = load_dev(slot);
+        }
+        if (ready == 0u) {
+          s_err = 1;
+          raise_error(a.sync, kErrHTimeout);
+        }
+      }
+      compiler_fence();
+      fetch_h();
+    } else {
+#pragma unroll
+      for (int u = 0; u < kHB; ++u) hv[u] = a.H[min((int)threadIdx.x + 256 * u, a.M * a.r - 1)];
+      h_have = true;
+    }
+  };
+
+  // Outliers: corr[i] = sum over the thread's entries of delta * x[i, col], summed over the
+  // TPR threads of the row by a butterfly (each holds the row's sum).
+  float corr[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) corr[i] = 0.f;
+  auto outlier_pass = [&]() __attribute__((always_inline)) {
+    if (!csr) return;
+    const int xc0 = s0 * 128;
+    auto entry = [&](uint32_t col, float d) __attribute__((always_inline)) {
+      const int xi = (int)col - xc0;  // activations are staged in natural column order
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        if (i < a.M) corr[i] += d * h2f(xs[i * a.xstride + xi]);
+    };
+#pragma unroll
+    for (int u = 0; u < kEB; ++u)
+      if (e0 + jr + TPR * u < e1) entry(ecol[u], edel[u]);
+    for (int e = e0 + jr + TPR * kEB; e < e1; e += TPR) entry(a.gcol[e], a.delta[e]);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      if (i < a.M) {
+        float v = corr[i];
+#pragma unroll
+        for (int m = TPR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+        corr[i] = v;
+      }
+    }
+  };
+
   // Steady state: every slot consumed is reloaded kPF slabs ahead; then one round with
   // conditional reloads and a last round without (nw is wave-uniform).
   int j0 = 0;
@@ -468,81 +551,29 @@ void stream4_kernel(const StreamArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) red[((wave * NA + g) * 4 + e) * 64 + lane] = acc[g][e];
 
-  // DoRA H into registers.  A caller's H, or (one K split: this block finishes its rows) the
-  // computed H, is loaded now so the loads complete while the outlier pass runs; with several
-  // splits only the last to arrive needs H and loads it then.  Computed H: each wave first
-  // waits for the block's ready slot (normally raised long before; after spin_limit polls the
-  // wait gives up, raises kErrHTimeout and the block writes NaN rows rather than hang).  A
-  // block polls before it counts itself on the slot, so no slot is lowered while one of its
-  // tile blocks still polls.
-  const int slots = min(a.TB, kMaxSlots);
-  uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
-  constexpr int kHB = (MB * kMaxRank + 255) / 256;  // H words per thread (M * r <= MB * 64)
-  float hv[kHB];
-  // Only the threads that own H elements load them (the others return; store_h and the
-  // epilogue go through LDS after a barrier).  Thread 0 also reads the workspace's sticky
-  // error word, in parallel with H (no extra round trip).
-  auto load_h = [&]() __attribute__((always_inline)) {
-    if ((int)threadIdx.x >= a.M * a.r) return;
-    if (a.h_blocks > 0) {
-      if (lane == 0) {
-        uint32_t ready = load_dev(slot);
-        for (uint32_t spins = 0; ready == 0u && spins < a.spin_limit; ++spins) {
-          __builtin_amdgcn_s_sleep(2);
-          ready = load_dev(slot);
-        }
-        if (ready == 0u) {
-          s_err = 1;
-          raise_error(a.sync, kErrHTimeout);
-        }
-      }
-      compiler_fence();
-      uint32_t err = 0u;
-      if (threadIdx.x == 0) err = load_dev(a.sync + kSyncErr);
-#pragma unroll
-      for (int u = 0; u < kHB; ++u) hv[u] = load_dev(a.hfin + min((int)threadIdx.x + 256 * u, a.M * a.r - 1));
-      if (err != 0u) s_err = 1;
-    } else {
-#pragma unroll
-      for (int u = 0; u < kHB; ++u) hv[u] = a.H[min((int)threadIdx.x + 256 * u, a.M * a.r - 1)];
-    }
-  };
   auto store_h = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kHB; ++u)
       if ((int)threadIdx.x + 256 * u < a.M * a.r) hs[threadIdx.x + 256 * u] = hv[u];
   };
+  // One K split (or H given): this block finishes its rows and needs H now; the loads overlap
+  // the outlier pass when it has not run yet.  Several splits: only the last to arrive needs H.
   const bool h_early = a.r > 0 && (a.splits == 1 || a.h_blocks == 0);
   if (h_early) load_h();
-
-  // Outliers: corr[i] = sum over the thread's entries of delta * x[i, col].
-  float corr[MB];
-#pragma unroll
-  for (int i = 0; i < MB; ++i) corr[i] = 0.f;
-  if (csr) {
-    const int xc0 = s0 * 128;
-    auto entry = [&](uint32_t col, float d) __attribute__((always_inline)) {
-      const int xc = (int)col - xc0;
-      const int xi = xc;  // activations are staged in natural column order
-#pragma unroll
-      for (int i = 0; i < MB; ++i)
-        if (i < a.M) corr[i] += d * h2f(xs[i * a.xstride + xi]);
-    };
-#pragma unroll
-    for (int u = 0; u < kEB; ++u)
-      if (e0 + jr + TPR * u < e1) entry(ecol[u], edel[u]);
-    for (int e = e0 + jr + TPR * kEB; e < e1; e += TPR) entry(a.gcol[e], a.delta[e]);
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-      if (i < a.M) {
-        float v = corr[i];
-#pragma unroll
-        for (int m = TPR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-        corr[i] = v;
-      }
-    }
-  }
+  outlier_pass();
   __syncthreads();
+  // Count the block as a consumer of its ready slot as soon as every wave's poll is done (the
+  // barrier above), so the atomic's round trip overlaps the epilogue; the slot's last
+  // consumer lowers it at the end, for the next call.
+  uint32_t cons_old = 0u;
+  bool counted = false;
+  auto count_consumer = [&]() __attribute__((always_inline)) {
+    if (h_fused && threadIdx.x == 0) {
+      cons_old = atomicAdd(slot + 1, 1u);
+      counted = true;
+    }
+  };
+  if (h_early) count_consumer();
 
   // Wave partial of output (i, row rr) in phase p.
   auto red_at = [&](int i, int rr, int p) __attribute__((always_inline)) -> float& {
@@ -648,6 +679,7 @@ void stream4_kernel(const StreamArgs a) {
       store_h();
     }
     __syncthreads();
+    if (!h_early) count_consumer();
   }
 
   // Epilogue: y = fp16_rn((v + s * H[i, :] . B[n, :]) * gamma[n]) with H, B and gamma from LDS;
@@ -681,13 +713,11 @@ void stream4_kernel(const StreamArgs a) {
       }
     }
   }
-  if (a.r > 0 && a.h_blocks > 0 && threadIdx.x == 0) {
-    // count this consumer; the slot's last consumer lowers it for the next call
+  if (counted) {  // the slot's last consumer lowers it for the next call
     const int g = tb % slots;
     const uint32_t members = (uint32_t)(a.TB / slots + (g < a.TB % slots ? 1 : 0));
-    const uint32_t old = atomicAdd(slot + 1, 1u);
-    if (old >= members) raise_error(a.sync, kErrArrivals);
-    if (old == members - 1u) {
+    if (cons_old >= members) raise_error(a.sync, kErrArrivals);
+    if (cons_old == members - 1u) {
       store_dev(slot + 1, 0u);
       store_dev(slot, 0u);
     }
