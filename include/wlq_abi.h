@@ -143,15 +143,18 @@ size_t wlq_prepared_bytes(int64_t N, int64_t K, int32_t bits, int32_t group_size
  * 128-column tiles in MFMA lane order (3-bit codes widened to 4-bit nibbles, their
  * 8-entry LUTs zero-padded to 16), LUT byte planes per 16-row tile, and per
  * outlier its column and the fp32 delta fp16(e5m2 << 8) - lut[code] of the
- * reference's GEMV outlier correction (csrc/gemv_kernel.cu:262-288). */
+ * reference's GEMV outlier correction (csrc/gemv_kernel.cu:262-288), and the
+ * outliers once more as overwrite patches grouped by (16-row tile, 128-column slab)
+ * for the M = 9..128 kernel. */
 int wlq_prepare(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K, int32_t bits, int32_t group_size,
                 const int32_t* chunk_offsets, const uint16_t* chunk_cols, const uint8_t* chunk_vals, int64_t nnz,
                 void* prepared, size_t prepared_bytes, hipStream_t stream);
 
-/* wlq_gemm with the layer's prepared layout: M <= 32 runs the streaming decode
+/* wlq_gemm with the layer's prepared layout: M <= 8 runs the streaming decode
  * kernel on `prepared` (plus the reference chunk offsets) where its activation
- * staging fits (3-bit: not at M = 13..16 and 26..32), every other case the same
- * kernels as wlq_gemm on the reference-format tensors, which stay required.
+ * staging fits, M = 9..128 the kernel that streams the activations through LDS
+ * slab by slab (its outliers come from the prepared patch lists), every other case
+ * the same kernels as wlq_gemm on the reference-format tensors, which stay required.
  * Replaces the same reference launchers as wlq_gemm / wlq_gemv
  * (csrc/vllm_binding.cpp:10-52, :318-419). */
 int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c, const void* prepared,

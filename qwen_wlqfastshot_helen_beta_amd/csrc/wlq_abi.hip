@@ -60,6 +60,9 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int words)
 }
 
 constexpr int kMaxDevices = 64;
+// Prepared-layout products with more activation rows than this run the wide kernel
+// (activations streamed through LDS) up to wide_max_m(); up to this many, the decode kernel.
+constexpr int64_t kWideMinM = 8;
 std::atomic<int> g_cu_count[kMaxDevices];
 
 int cu_count_for(int device) {
@@ -240,8 +243,10 @@ int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c
                       fn, &L);
   if (st != WLQ_OK) return st;
   const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_A, lora_scale, r);
-  if (prepared != nullptr && M >= 1 && M <= wlq::stream_max_m() && L.N > 0 && X != nullptr && out != nullptr &&
-      wlq::prepared_supported(L.N, L.K, L.bits, L.group_size) && nnz >= 0 && (L.offsets != nullptr || nnz == 0)) {
+  const bool wide = M > kWideMinM && M <= wlq::wide_max_m();
+  if (prepared != nullptr && M >= 1 && (M <= wlq::stream_max_m() || wide) && L.N > 0 && X != nullptr &&
+      out != nullptr && wlq::prepared_supported(L.N, L.K, L.bits, L.group_size) && nnz >= 0 &&
+      (L.offsets != nullptr || nnz == 0)) {
     const size_t need = wlq::prepared_layout(L.N, L.K, L.group_size, nnz).bytes;
     if (prepared_bytes < need) {
       wlq::set_error("%s: the prepared buffer holds %zu bytes, the layer needs %zu (nnz=%lld)", fn, prepared_bytes,
@@ -254,10 +259,32 @@ int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c
                                       (reinterpret_cast<uintptr_t>(D.B) & 15u) == 0);
     const bool aligned = (reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (reinterpret_cast<uintptr_t>(prepared) & 255u) == 0 &&
                          (!fused_h || (reinterpret_cast<uintptr_t>(D.A) & 15u) == 0) && dora_ok;
+    const size_t ws = workspace != nullptr ? workspace_bytes : 0;
+    if (wide) {
+      const bool csr = L.offsets != nullptr && nnz > 0;
+      const wlq::WidePlan p =
+          wlq::plan_wide(L.N, L.K, (int)M, current_cu_count(), D.r, fused_h ? D.r : 0, L.chunk, csr);
+      const bool need_sync = p.splits > 1 || fused_h;
+      const bool ws_ok = !need_sync || ws >= wlq::kSyncBytes + p.workspace_bytes;
+      const bool runs = p.ok && aligned;
+      if (runs && !ws_ok && strict) {
+        wlq::set_error("%s: M=%lld N=%lld K=%lld needs %zu bytes of scratch, more than the %zu bytes it holds", fn,
+                       (long long)M, (long long)N, (long long)K, wlq::kSyncBytes + p.workspace_bytes, ws);
+        return WLQ_ERR_CAPACITY;
+      }
+      if (runs && ws_ok) {
+        char* wbase = reinterpret_cast<char*>(workspace);
+        uint32_t* sync = need_sync ? reinterpret_cast<uint32_t*>(wbase) : nullptr;
+        float* w = need_sync ? reinterpret_cast<float*>(wbase + wlq::kSyncBytes) : nullptr;
+        return hip_status(wlq::launch_wide(L, prepared, nnz, D, reinterpret_cast<const uint16_t*>(X),
+                                           reinterpret_cast<uint16_t*>(out), (int)M, p, w, sync, stream),
+                          fn);
+      }
+      return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, fn);
+    }
     const wlq::StreamPlan p =
         wlq::plan_stream(L.N, L.K, (int)M, current_cu_count(), fused_h ? D.r : 0, L.chunk);
     const bool need_sync = p.splits > 1 || fused_h;
-    const size_t ws = workspace != nullptr ? workspace_bytes : 0;
     const bool ws_ok = !need_sync || ws >= wlq::kSyncBytes + p.workspace_bytes;
     const bool runs = p.ok && aligned && (!fused_h || D.r <= wlq::stream_max_rank());
     if (runs && !ws_ok && strict) {
@@ -356,6 +383,11 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
     const wlq::StreamPlan sp = wlq::plan_stream((int)N, (int)K, (int)M, cus,
                                                 r > 0 && r <= wlq::stream_max_rank() ? r : 0, L.chunk);
     need = std::max(need, sp.workspace_bytes + 256);
+  }
+  if (M > kWideMinM && M <= wlq::wide_max_m() && (bits == 4 || bits == 3)) {  // or the wide kernel
+    const int rr = r > 0 && r <= wlq::stream_max_rank() ? r : 0;
+    const wlq::WidePlan wp = wlq::plan_wide((int)N, (int)K, (int)M, cus, rr, rr, L.chunk, true);
+    need = std::max(need, wp.workspace_bytes + 256);
   }
   return need > 0 ? wlq::kSyncBytes + need : 0;
 }

@@ -51,6 +51,12 @@ constexpr int kSyncWords = (int)(kSyncBytes / 4);
 // and write NaN too, until wlq_workspace_reset clears the area.
 constexpr int kSyncErrorWord = kSyncWords - 32;
 constexpr int kMaxSyncRowBlocks = kSyncErrorWord;
+// Counter words of the streaming kernels (decode and wide), all zero between calls:
+constexpr int kSyncDora = 0;      // DoRA blocks arrived (reset by the last of them)
+constexpr int kSyncSlot0 = 64;    // H ready slots: word 0 = H published, word 1 = consumers counted
+constexpr int kSlotWords = 16;    // one 64-byte line per slot
+constexpr int kMaxSlots = 128;    // tile block tb uses slot tb % min(TB, kMaxSlots)
+constexpr int kSyncTile = kSyncSlot0 + kSlotWords * kMaxSlots;  // [TB] split arrivals per tile block
 constexpr uint32_t kErrHTimeout = 1u;   // a wait for the DoRA H ran out of polls
 constexpr uint32_t kErrArrivals = 2u;   // an arrival count exceeded what one call makes
 constexpr uint32_t kDefaultSpinLimit = 1u << 24;  // ~1 s of polls
@@ -81,7 +87,7 @@ hipError_t launch_dequant(const Layer& L, uint16_t* W, hipStream_t stream);
 // (wlq_stream.hip): byte offsets of its four parts inside one buffer.
 struct PreparedLayout {
   int T, S, ng;             // row tiles of 16, slabs of 128 columns, LUT groups per row
-  size_t codes_off, planes_off, gcol_off, delta_off, bytes;
+  size_t codes_off, planes_off, gcol_off, delta_off, wpidx_off, wpatch_off, bytes;
 };
 bool prepared_supported(int N, int K, int bits, int group_size);
 PreparedLayout prepared_layout(int N, int K, int group_size, int64_t nnz);
@@ -100,6 +106,22 @@ StreamPlan plan_stream(int N, int K, int M, int cu_count, int fused_rank, int ch
 hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, const Dora& D, const uint16_t* x,
                          uint16_t* out, int M, const StreamPlan& plan, float* workspace, uint32_t* sync,
                          hipStream_t stream);
+
+// Product for 8 < M <= wide_max_m() on the prepared layout (wlq_wide.hip): activations streamed
+// through LDS slab by slab, outliers overwritten in the dequantized words.
+struct WidePlan {
+  int TB, splits, sps;      // 64-row tile blocks, K splits, 128-column slabs per split
+  int h_kb, h_blocks;       // DoRA column blocks (512 columns) and DoRA blocks (x 32-row chunks of M)
+  size_t hfin_off, hpart_off, partial_off, workspace_bytes;
+  size_t lds;               // dynamic LDS bytes per block
+  bool ok;
+};
+int wide_max_m();
+// rank: DoRA rank of the epilogue (0: none); fused_rank: rank when H is computed in the kernel.
+WidePlan plan_wide(int N, int K, int M, int cu_count, int rank, int fused_rank, int chunk, bool csr);
+hipError_t launch_wide(const Layer& L, const void* prepared, int64_t nnz, const Dora& D, const uint16_t* x,
+                       uint16_t* out, int M, const WidePlan& plan, float* workspace, uint32_t* sync,
+                       hipStream_t stream);
 
 // out = fp16_rn(sum of fp32 split-K partials [splits, M, N]) (epilogue already applied).
 hipError_t launch_splitk_sum(const float* partial, int splits, int M, int N, uint16_t* out, hipStream_t stream);

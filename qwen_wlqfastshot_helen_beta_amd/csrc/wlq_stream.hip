@@ -26,6 +26,16 @@
 //   gcol   u16 [nnz]            the outlier's column (chunk base + chunk column).
 //   delta  f32 [nnz]            fp32(fp16(e5m2 << 8)) - fp32(lut[code]): the
 //                               reference's delta_w, computed once.
+//   wpidx  u32 [T*S + 1]        start of each (tile, slab)'s patch list in wpatch
+//                               (exclusive prefix sums; the last entry is the total).
+//   wpatch u32 [nnz]            the outliers as patches of the dequantized operand of
+//                               the M = 9..128 kernel (wlq_wide.hip), grouped by
+//                               (tile, slab) in storage order: lane | (column % 32) << 6
+//                               | e5m2 byte << 24, lane = row % 16 + 16 ((column % 128) / 32)
+//                               -- the MFMA B-operand lane holding that column.  Entries
+//                               with column >= K are dropped, and so is an entry whose
+//                               column a later entry of the row overwrites (the last
+//                               write wins, as in the dense overwrite).
 // The reference's chunk offsets are used as they are.
 //
 // Work decomposition.  The grid is the DoRA blocks (x.A^T partial sums over 512
@@ -83,13 +93,8 @@ constexpr int kHCols = 512;     // columns per DoRA block
 constexpr int kMaxRank = 64;
 constexpr int kXBudget = 16384; // activation staging bytes per block
 constexpr int kBlocksPerCU = WLQ_STREAM_BLOCKS_PER_CU;  // tile-block target per CU
-// Sync words in the workspace's counter area (all zero between calls).
-constexpr int kSyncDora = 0;      // DoRA blocks arrived (reset by the last of them)
+// Sync words in the workspace's counter area (layout in wlq_internal.h; all zero between calls).
 constexpr int kSyncErr = kSyncErrorWord;  // sticky error bits (own 128-byte line)
-constexpr int kSyncSlot0 = 64;    // ready slots: word 0 = H published, word 1 = consumers counted
-constexpr int kSlotWords = 16;    // one 64-byte line per slot
-constexpr int kMaxSlots = 128;    // tile block tb uses slot tb % min(TB, kMaxSlots)
-constexpr int kSyncTile = kSyncSlot0 + kSlotWords * kMaxSlots;  // [TB] split arrivals per tile block
 
 struct StreamArgs {
   const u32x4_t* codes;
@@ -827,6 +832,72 @@ __global__ __launch_bounds__(256) void prep_outliers_kernel(const uint32_t* __re
   }
 }
 
+// Patch lists of the M = 9..128 kernel, one thread per (tile t, slab s): the entries of
+// the tile's 16 rows in the chunk holding the slab, kept when they fall in the slab,
+// inside K and are not overwritten by a later entry of the row.  COUNT pass: wpidx[ts] =
+// number kept; FILL pass (after the scan): the patches at wpidx[ts] onwards.
+template <bool FILL>
+__global__ __launch_bounds__(256) void prep_wpatch_kernel(const int32_t* __restrict__ offsets,
+                                                          const uint16_t* __restrict__ cols,
+                                                          const uint8_t* __restrict__ vals, int N, int K, int nch,
+                                                          int chunk, int T, int S, uint32_t* __restrict__ wpidx,
+                                                          uint32_t* __restrict__ wpatch) {
+  const size_t total = (size_t)T * S;
+  const int spc = chunk / 128;
+  for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
+    const int t = (int)(idx / (size_t)S);
+    const int s = (int)(idx - (size_t)t * S);
+    const int c = s / spc;
+    const int sc = s - c * spc;  // slab within the chunk
+    uint32_t pos = FILL ? wpidx[idx] : 0u;
+    for (int rr = 0; rr < 16; ++rr) {
+      const int n = 16 * t + rr;
+      if (n >= N) break;
+      const int32_t* offr = offsets + (size_t)n * (nch + 1);
+      const int e_lo = offr[c];
+      const int e_hi = offr[c + 1];
+      for (int e = e_lo; e < e_hi; ++e) {
+        const int cl = (int)cols[e];
+        if (cl >= chunk || c * chunk + cl >= K || (cl >> 7) != sc) continue;
+        bool later = false;
+        for (int e2 = e + 1; e2 < e_hi && !later; ++e2) later = (int)cols[e2] == cl;
+        if (later) continue;
+        if (FILL) {
+          const uint32_t cs = (uint32_t)cl & 127u;
+          wpatch[pos] = ((uint32_t)rr + 16u * (cs >> 5)) | ((cs & 31u) << 6) | ((uint32_t)vals[e] << 24);
+        }
+        ++pos;
+      }
+    }
+    if (!FILL) wpidx[idx] = pos;
+  }
+}
+
+// In-place exclusive prefix sums of v[0, n) by one block; v[n] = the total.
+__global__ __launch_bounds__(1024) void prep_scan_kernel(uint32_t* __restrict__ v, int n) {
+  __shared__ uint32_t part[1024];
+  const int per = (n + 1023) / 1024;
+  const int b = (int)threadIdx.x * per;
+  const int e = min(n, b + per);
+  uint32_t sum = 0u;
+  for (int i = b; i < e; ++i) sum += v[i];
+  part[threadIdx.x] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const uint32_t add = threadIdx.x >= (unsigned)off ? part[threadIdx.x - off] : 0u;
+    __syncthreads();
+    part[threadIdx.x] += add;
+    __syncthreads();
+  }
+  uint32_t run = part[threadIdx.x] - sum;
+  for (int i = b; i < e; ++i) {
+    const uint32_t c = v[i];
+    v[i] = run;
+    run += c;
+  }
+  if (threadIdx.x == 1023) v[n] = part[1023];
+}
+
 template <int LM, int TPB, int MB>
 hipError_t launch_tpl(const StreamArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
   hipLaunchKernelGGL((stream4_kernel<LM, TPB, MB>), grid, dim3(256), lds, stream, a);
@@ -854,7 +925,9 @@ PreparedLayout prepared_layout(int N, int K, int group_size, int64_t nnz) {
   p.planes_off = align256((size_t)p.T * p.S * 1024);
   p.gcol_off = p.planes_off + align256((size_t)p.T * p.ng * 512);
   p.delta_off = p.gcol_off + align256((size_t)nnz * 2);
-  p.bytes = p.delta_off + align256((size_t)nnz * 4);
+  p.wpidx_off = p.delta_off + align256((size_t)nnz * 4);
+  p.wpatch_off = p.wpidx_off + align256(((size_t)p.T * p.S + 1) * 4);
+  p.bytes = p.wpatch_off + align256((size_t)nnz * 4);
   return p;
 }
 
@@ -875,6 +948,21 @@ hipError_t launch_prepare(const Layer& L, int64_t nnz, void* prepared, hipStream
     hipLaunchKernelGGL(prep_outliers_kernel, grid_for((size_t)L.N * L.nch), dim3(256), 0, stream, L.q, L.lut,
                        L.offsets, L.cols, L.vals, L.N, L.K, L.wpr, L.bits, ng, L.group_size, L.nch, L.chunk,
                        reinterpret_cast<uint16_t*>(base + p.gcol_off), reinterpret_cast<float*>(base + p.delta_off));
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // patch lists: counts per (tile, slab), prefix sums in place, then the patches
+    uint32_t* wpidx = reinterpret_cast<uint32_t*>(base + p.wpidx_off);
+    uint32_t* wpatch = reinterpret_cast<uint32_t*>(base + p.wpatch_off);
+    const size_t ts = (size_t)p.T * p.S;
+    hipLaunchKernelGGL(prep_wpatch_kernel<false>, grid_for(ts), dim3(256), 0, stream, L.offsets, L.cols, L.vals, L.N,
+                       L.K, L.nch, L.chunk, p.T, p.S, wpidx, wpatch);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(prep_scan_kernel, dim3(1), dim3(1024), 0, stream, wpidx, (int)ts);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(prep_wpatch_kernel<true>, grid_for(ts), dim3(256), 0, stream, L.offsets, L.cols, L.vals, L.N,
+                       L.K, L.nch, L.chunk, p.T, p.S, wpidx, wpatch);
     e = hipGetLastError();
   }
   return e;

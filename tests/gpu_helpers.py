@@ -144,9 +144,55 @@ def prepared_reference(L: synth.SynthLayer):
     return codes, planes, gcol, delta
 
 
+def wide_patches_reference(N: int, K: int, bits: int, offsets, cols, vals):
+    """numpy rebuild of the prepared layout's patch lists (the M = 9..128 kernel's
+    outliers): (wpidx u32 [T*S + 1], wpatch u32 [kept]).  Entries with column < K and
+    chunk column < the chunk width, minus those a later entry of the same row overwrites,
+    grouped by (tile t = row // 16, slab s = column // 128) in (row, storage) order; patch
+    = lane | (column % 32) << 6 | e5m2 byte << 24 with lane = row % 16 + 16 ((column %
+    128) // 32)."""
+    T, S = -(-N // 16), -(-K // 128)
+    C = O.chunk_width(bits)
+    ent, rows, gcols = O.csr_to_coo(offsets, cols, C)
+    cols = np.asarray(cols).astype(np.int64)
+    ok = (cols[ent] < C) & (gcols < K)
+    # last write wins: drop an entry when a later one of the row has the same column
+    key = rows * (1 << 20) + gcols
+    last = np.ones(ent.size, dtype=bool)
+    order = np.lexsort((ent, key))
+    ks = key[order]
+    last[order[:-1]] = ks[:-1] != ks[1:]
+    keep = ok & last
+    ent, rows, gcols = ent[keep], rows[keep], gcols[keep]
+    t, s = rows // 16, gcols // 128
+    order = np.lexsort((ent, rows, s, t))
+    ent, rows, gcols, t, s = ent[order], rows[order], gcols[order], t[order], s[order]
+    cs = gcols % 128
+    lane = rows % 16 + 16 * (cs // 32)
+    wpatch = (lane | ((cs % 32) << 6) | (np.asarray(vals).astype(np.int64)[ent] << 24)).astype(np.uint32)
+    counts = np.bincount(t * S + s, minlength=T * S)
+    wpidx = np.zeros(T * S + 1, dtype=np.uint32)
+    wpidx[1:] = np.cumsum(counts)
+    return wpidx, wpatch
+
+
+def apply_wide_patches(W: np.ndarray, wpidx: np.ndarray, wpatch: np.ndarray, K: int) -> np.ndarray:
+    """What the wide kernel does with the patch lists, on a dense fp16 W [N, K]: patch p of
+    (tile t, slab s) writes fp16 bits (p >> 24) << 8 into row 16 t + (p & 15), column
+    128 s + 32 ((p & 63) >> 4) + ((p >> 6) & 31)."""
+    W = W.copy().view(np.uint16)
+    S = -(-K // 128)
+    for ts in range(wpidx.size - 1):
+        t, s = divmod(ts, S)
+        for p in wpatch[wpidx[ts]:wpidx[ts + 1]].astype(np.int64):
+            lane = p & 63
+            W[16 * t + (lane & 15), 128 * s + 32 * (lane >> 4) + ((p >> 6) & 31)] = (p >> 24) << 8
+    return W.view(np.float16)
+
+
 def split_prepared(buf: np.ndarray, L: synth.SynthLayer):
-    """Cut a prepared buffer (uint8) into its four parts (offsets as documented in
-    include/wlq_abi.h: 256-byte aligned, codes | planes | gcol | delta)."""
+    """Cut a prepared buffer (uint8) into its six parts (offsets as documented in
+    include/wlq_abi.h: 256-byte aligned, codes | planes | gcol | delta | wpidx | wpatch)."""
     N, K = L.N, L.K
     T, S = -(-N // 16), -(-K // 128)
     ng = 1 if L.group_size <= 0 or L.group_size >= K else -(-K // L.group_size)
@@ -154,11 +200,15 @@ def split_prepared(buf: np.ndarray, L: synth.SynthLayer):
     o_pl = a(T * S * 1024)
     o_gc = o_pl + a(T * ng * 512)
     o_dl = o_gc + a(L.nnz * 2)
+    o_wi = o_dl + a(L.nnz * 4)
+    o_wp = o_wi + a((T * S + 1) * 4)
     codes = buf[:T * S * 1024].view(np.uint32).reshape(T, S, 64, 4)
     planes = buf[o_pl:o_pl + T * ng * 512].reshape(T, ng, 2, 16, 16)
     gcol = buf[o_gc:o_gc + L.nnz * 2].view(np.uint16)
     delta = buf[o_dl:o_dl + L.nnz * 4].view(np.float32)
-    return codes, planes, gcol, delta
+    wpidx = buf[o_wi:o_wi + (T * S + 1) * 4].view(np.uint32)
+    wpatch = buf[o_wp:o_wp + L.nnz * 4].view(np.uint32)
+    return codes, planes, gcol, delta, wpidx, wpatch
 
 
 def run_prepared(vw, L: synth.SynthLayer, x: np.ndarray, dora: str = "fused", with_csr: bool = True, prep=None,

@@ -1,5 +1,5 @@
-"""GPU parity of the prepared-layout decode kernel (wlq_stream.hip) against the
-CPU oracle: the prepared layout itself bit-exact against a numpy rebuild, layer
+"""GPU parity of the prepared-layout products (wlq_stream.hip for M <= 8, wlq_wide.hip
+for M = 9..128) against the CPU oracle: the prepared layout itself bit-exact against a numpy rebuild, layer
 outputs within the tolerance of tests/gpu_helpers.py, across M = 1..32, LUT
 group sizes, ragged shapes, outliers on/off (incl. heavy rows), DoRA fused / H
 given / off, split-K, counter reset between calls, graph replay, determinism,
@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from gpu_helpers import (DEV, check_close, oracle_product, prepared_reference, run_prepared, run_product,
-                         split_prepared)
+                         split_prepared, wide_patches_reference)
 from qwen_wlqfastshot_helen_beta_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -35,6 +35,10 @@ def test_prepared_layout_bit_exact(vw, bits, gs):
         assert np.array_equal(got[1], ref[1]), "planes"
         assert np.array_equal(got[2].astype(np.int64), ref[2]), "gcol"
         assert np.array_equal(got[3].view(np.uint32), ref[3].view(np.uint32)), "delta"
+        if L.nnz > 0:
+            wpidx, wpatch = wide_patches_reference(N, K, bits, L.offsets, L.cols, L.vals)
+            assert np.array_equal(got[4], wpidx), "patch-list starts"
+            assert np.array_equal(got[5][:wpatch.size], wpatch), "patches"
 
 
 def test_prepare_unsupported_formats(vw):
@@ -64,9 +68,8 @@ def test_prepared_parity(vw, M):
 
 @pytest.mark.parametrize("M", [1, 2, 4, 8, 12, 13, 16, 17, 25, 26, 32])
 def test_prepared_parity_3bit(vw, M):
-    """3-bit layers: codes widened to nibbles, 640-column outlier chunks (5 slabs);
-    M = 13..16 and 26..32 exceed the kernel's activation staging for a 640-column chunk
-    and run the row-aligned kernel instead (same results either way)."""
+    """3-bit layers: codes widened to nibbles, 640-column outlier chunks (5 slabs); M <= 8
+    on the decode kernel, M >= 9 on the M = 9..128 kernel."""
     for gs in (0, 64, 128):
         for dora in ("fused", "h"):
             _case(M=M, gs=gs, dora=dora, bits=3)

@@ -124,13 +124,13 @@ def test_abi_workspace_status_without_counter_area():
 
 def test_abi_prepared_bytes():
     """Size of the prepared layout (host query, no GPU): 256-byte aligned parts
-    codes | planes | gcol | delta; 0 for formats without one."""
+    codes | planes | gcol | delta | patch-list starts | patches; 0 for formats without one."""
     lib = load_abi()
     a = lambda v: (v + 255) // 256 * 256  # noqa: E731
     for N, K, G, nnz in ((37888, 3584, 128, 678960), (77, 1000, 32, 100), (16, 512, 0, 0), (5, 8, 128, 1)):
         T, S = -(-N // 16), -(-K // 128)
         ng = 1 if G == 0 or G >= K else -(-K // G)
-        want = a(T * S * 1024) + a(T * ng * 512) + a(nnz * 2) + a(nnz * 4)
+        want = a(T * S * 1024) + a(T * ng * 512) + a(nnz * 2) + a(nnz * 4) + a((T * S + 1) * 4) + a(nnz * 4)
         assert lib.wlq_prepared_bytes(N, K, 4, G, nnz) == want, (N, K, G)
         # 3-bit: the same layout (codes as 4-bit nibbles, LUTs padded to 16); groups of >= 40 columns
         assert lib.wlq_prepared_bytes(N, K, 3, G, nnz) == (0 if 0 < G < 40 and G < K else want), (N, K, G)

@@ -1,4 +1,5 @@
-"""CPU pin of the prepared layout's selector-ready code encoding and its decode sequence.
+"""CPU pins of the prepared layout: the selector-ready code encoding and its decode
+sequence, and the outlier patch lists of the M = 9..128 kernel.
 
 The decode kernel expands one 32-bit word into 8 fp16 weights with five selector ops,
 twelve V_PERM_B32 and four ANDs (wlq_device.h, dequant_word4s).  This test emulates that
@@ -10,8 +11,11 @@ value at every position and for random words and LUTs."""
 from __future__ import annotations
 
 import numpy as np
+import pytest
 
-from gpu_helpers import selector_encode
+from gpu_helpers import apply_wide_patches, selector_encode, wide_patches_reference
+from oracle import wlq_oracle as O
+from qwen_wlqfastshot_helen_beta_amd import synth
 
 
 def v_perm(src0: np.ndarray, src1: np.ndarray, sel: np.ndarray) -> np.ndarray:
@@ -97,3 +101,65 @@ def test_random_words_and_luts():
     lo3, hi3 = planes(lut3)
     got3 = dequant_word4s(selector_encode(c3), lo3, hi3)
     assert np.array_equal(got3, np.take_along_axis(lut3.view(np.uint16), c3.astype(np.int64), axis=1))
+
+
+def _dense_without_outliers(L):
+    return O.dequant(L.q, L.lut, L.N, L.K, L.bits, group_size=L.group_size)
+
+
+def _with_csr(L, offsets, cols, vals):
+    return O.dequant(L.q, L.lut, L.N, L.K, L.bits, offsets, cols, vals, group_size=L.group_size)
+
+
+@pytest.mark.parametrize("N,K,bits,gs,density,heavy", [
+    (77, 1000, 4, 128, 0.02, 0.0),   # ragged rows and slabs, K not a multiple of 128
+    (64, 3584, 4, 0, 0.005, 0.1),    # heavy rows
+    (40, 1928, 3, 64, 0.03, 0.0),    # 3-bit: 640-column chunks (5 slabs)
+    (32, 1024, 4, 128, 0.2, 0.0),    # > 256 patches in one 16 x 128 block
+])
+def test_wide_patch_lists_reproduce_the_overwrite(N, K, bits, gs, density, heavy):
+    """The prepared layout's patch lists (numpy builder of the device layout), applied the
+    way the M = 9..128 kernel applies them (lane and element decoded from the patch), turn
+    the LUT-only W0 into the oracle's W0 with the outlier overwrite, bit for bit."""
+    L = synth.make_layer(N=N, K=K, bits=bits, group_size=gs, rank=0, density=density, seed=N + K,
+                         heavy_frac=heavy)
+    wpidx, wpatch = wide_patches_reference(N, K, bits, L.offsets, L.cols, L.vals)
+    assert wpidx[-1] == wpatch.size <= L.nnz
+    got = apply_wide_patches(_dense_without_outliers(L), wpidx, wpatch, K)
+    want = O.dequant(L.q, L.lut, N, K, bits, L.offsets, L.cols, L.vals, group_size=gs)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    if density >= 0.2:
+        assert np.diff(wpidx).max() > 256  # the kernel's global-memory overflow path is exercised
+
+
+def test_wide_patch_lists_edge_entries():
+    """Last write wins for a repeated column, a column >= K is dropped (as the dense
+    overwrite does), and the lists group by (tile, slab) in row order."""
+    N, K, bits = 20, 1000, 4
+    C = O.chunk_width(bits)
+    L = synth.make_layer(N=N, K=K, bits=bits, group_size=128, rank=0, density=0.0, seed=5)
+    # row 3: column 7 twice (values 0x3C then 0x40), column 130; row 17: column 999 and
+    # chunk column C - 1 of the last chunk (column 1023 >= K: dropped)
+    nch = -(-K // C)
+    offsets = np.zeros((N, nch + 1), dtype=np.int32)
+    entries = {3: [(0, 7, 0x3C), (0, 7, 0x40), (0, 130, 0x44)], 17: [(1, 999 - C, 0x48), (1, C - 1, 0x7C)]}
+    cols, vals, pos = [], [], 0
+    for n in range(N):
+        for c in range(nch):
+            offsets[n, c] = pos
+            for cc, col, v in entries.get(n, []):
+                if cc == c:
+                    cols.append(col)
+                    vals.append(v)
+                    pos += 1
+        offsets[n, nch] = pos
+    cols = np.array(cols, dtype=np.uint16)
+    vals = np.array(vals, dtype=np.uint8)
+    wpidx, wpatch = wide_patches_reference(N, K, bits, offsets, cols, vals)
+    assert wpatch.size == 3  # one of the two column-7 entries and the column >= K are gone
+    got = apply_wide_patches(_dense_without_outliers(L), wpidx, wpatch, K)
+    want = _with_csr(L, offsets, cols, vals)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    assert got.view(np.uint16)[3, 7] == 0x4000  # the later value
+    S = -(-K // 128)
+    assert [int(wpidx[t * S + s + 1] - wpidx[t * S + s]) for t, s in ((0, 0), (0, 1), (1, 7))] == [1, 1, 1]
