@@ -83,6 +83,19 @@ int wlq_repack_row_aligned(const uint32_t* src, int64_t src_words, int64_t N, in
   }
   const int64_t spw = wlq::symbols_per_word(bits);
   const uint32_t mask = (1u << bits) - 1u;
+  if (K % spw == 0 && K / spw == wpr) {
+    // every row is whole source words with no padding (Qwen2.5's K at 4 bits): the layouts
+    // coincide word for word (3-bit: the two unused top bits cleared as the repack leaves them)
+    const int64_t need = N * wpr;
+    const int64_t have = std::min(need, src_words);
+    if (bits == 3) {
+      for (int64_t w = 0; w < have; ++w) dst[w] = src[w] & 0x3FFFFFFFu;
+    } else if (have > 0) {
+      std::memcpy(dst, src, sizeof(uint32_t) * (size_t)have);
+    }
+    if (need > have) std::memset(dst + have, 0, sizeof(uint32_t) * (size_t)(need - have));
+    return WLQ_OK;
+  }
   std::memset(dst, 0, sizeof(uint32_t) * (size_t)(N * wpr));
   int64_t f = 0;  // flat symbol index in the source stream
   for (int64_t n = 0; n < N; ++n) {

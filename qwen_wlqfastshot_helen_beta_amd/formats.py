@@ -95,6 +95,54 @@ def fp16_to_e5m2_u8(values_fp16: np.ndarray) -> np.ndarray:
     return np.clip((u16 + 0x80) >> 8, 0, 255).astype(np.uint8)
 
 
+def ef_encode_coords(rows: np.ndarray, cols: np.ndarray, N: int, K: int, tile_size: int = 64):
+    """Outlier positions -> the checkpoint's Elias-Fano tiles (``ef_tile_meta`` int64
+    ``[tiles, 2]`` = (start bit, count), ``ef_bitstream`` uint32), the format the loader
+    decodes (vllm_wlq/linear_method.py:243-281, csrc/vllm_binding.cpp:94-196).
+
+    Tiles of ``tile_size``^2 cells in row-major tile order over the padded matrix; in a
+    tile the positions are local indices ``(row % T) * T + col % T`` in ascending order,
+    coded with L = max(0, floor(log2(T^2 / m))) low bits each (LSB first, one after
+    another), then the high parts ``index >> L`` in unary: a 0 per increment over the
+    previous element's, a 1 per element.  The stream is the tiles' codes back to back,
+    packed LSB first into 32-bit words (at least one).  Vectorized over all positions."""
+    rows = np.asarray(rows, dtype=np.int64).ravel()
+    cols = np.asarray(cols, dtype=np.int64).ravel()
+    T = int(tile_size)
+    U = T * T
+    nty, ntx = -(-N // T), -(-K // T)
+    ntiles = nty * ntx
+    tile = (rows // T) * ntx + cols // T
+    loc = (rows % T) * T + cols % T
+    order = np.lexsort((loc, tile))
+    tile, loc = tile[order], loc[order]
+    if tile.size > 1 and np.any((tile[1:] == tile[:-1]) & (loc[1:] == loc[:-1])):
+        raise ValueError("repeated outlier position")
+    m = np.bincount(tile, minlength=ntiles).astype(np.int64)
+    L = np.zeros(ntiles, dtype=np.int64)
+    nz = m > 0
+    L[nz] = np.maximum(0, np.floor(np.log2(U / m[nz].astype(np.float64)))).astype(np.int64)
+    first = np.zeros(ntiles + 1, dtype=np.int64)
+    first[1:] = np.cumsum(m)
+    rank = np.arange(tile.size, dtype=np.int64) - first[tile]
+    Le = L[tile]
+    high = loc >> Le
+    high_last = np.zeros(ntiles, dtype=np.int64)
+    high_last[nz] = high[first[1:][nz] - 1]  # ascending within a tile: the last is the largest
+    nbits = m * L + np.where(nz, high_last + m, 0)
+    start = np.zeros(ntiles, dtype=np.int64)
+    start[1:] = np.cumsum(nbits)[:-1]
+    total = int(nbits.sum())
+    bits = np.zeros(max(1, -(-total // 32)) * 32, dtype=np.uint8)
+    base = start[tile] + rank * Le
+    for b in range(int(L.max()) if ntiles else 0):
+        sel = Le > b
+        bits[base[sel] + b] = ((loc[sel] >> b) & 1).astype(np.uint8)
+    bits[start[tile] + m[tile] * Le + high + rank] = 1
+    meta = np.stack([start, m], axis=1)
+    return meta, np.packbits(bits, bitorder="little").view(np.uint32).copy()
+
+
 def chunk_csr_from_coords(rows: np.ndarray, cols: np.ndarray, N: int, K: int, chunk_m: int):
     """Sorted-or-not (row, col) outlier coordinates -> (offsets int32 [N, nch+1],
     chunk_cols uint16, order) where ``order`` is the permutation that puts the

@@ -161,6 +161,26 @@ def test_abi_host_helpers_match_oracle():
         # a destination that is too small is refused
         st = lib.wlq_repack_row_aligned(src.ctypes.data, src.size, N, K, bits, dst.ctypes.data, dst.size - 1)
         assert st == 4
+    # rows of whole, unpadded words (K a multiple of the codes per word, words per row a
+    # multiple of 4): the word-copy path, against the oracle's repack, incl. 3-bit words whose
+    # unused top bits are set in the source and a source one word short
+    for bits, K in ((4, 3584), (4, 64), (2, 256), (1, 128), (3, 1280)):
+        N = 6
+        codes = rng.integers(0, 1 << bits, (N, K)).astype(np.uint8)
+        src = O.pack_continuous(codes, bits).view(np.uint32).copy()
+        wpr = O.words_per_row(K, bits)
+        assert K % O.symbols_per_word(bits) == 0 and K // O.symbols_per_word(bits) == wpr
+        if bits == 3:
+            src |= np.uint32(0xC0000000)
+        want = O.pack_row_aligned(codes, bits)[0].view(np.uint32)
+        dst = np.full(N * wpr, 0xFFFFFFFF, dtype=np.uint32)
+        assert lib.wlq_repack_row_aligned(src.ctypes.data, src.size, N, K, bits, dst.ctypes.data, dst.size) == 0
+        assert np.array_equal(dst, want), (bits, K)
+        dst[:] = 0xFFFFFFFF
+        assert lib.wlq_repack_row_aligned(src.ctypes.data, src.size - 1, N, K, bits, dst.ctypes.data, dst.size) == 0
+        want_short = want.copy()
+        want_short[-1] = 0
+        assert np.array_equal(dst, want_short), (bits, K)
 
 
 def test_abi_ef_decoder_matches_oracle():

@@ -277,3 +277,25 @@ def test_ef_round_trip_random():
         off, cols = O.ef_decode_to_chunk_csr(meta, bs, H, W, T, 16)
         off2, cols2, _ = O.build_chunk_csr(mask, None, 16)
         assert np.array_equal(off, off2) and np.array_equal(cols, cols2)
+
+
+def test_ef_vectorized_encoder_matches_the_oracle():
+    """formats.ef_encode_coords (the checkpoint writer's encoder) emits the oracle encoder's
+    meta and bitstream bit for bit, including empty and full tiles and ragged edges, and the
+    hand-coded example above."""
+    from qwen_wlqfastshot_helen_beta_amd import formats
+
+    meta, bs = formats.ef_encode_coords([0, 1, 2], [1, 2, 3], 4, 4, 4)
+    assert meta.tolist() == [[0, 3]] and bs.tolist() == [0x579]
+    rng = np.random.default_rng(3)
+    for (H, W, T, d) in [(20, 37, 8, 0.1), (64, 64, 16, 0.02), (9, 100, 32, 0.5), (5, 5, 4, 1.0), (17, 40, 8, 0.0),
+                         (130, 200, 64, 0.005), (70, 65, 64, 0.3)]:
+        mask = rng.random((H, W)) < d
+        r, c = np.nonzero(mask)
+        perm = rng.permutation(r.size)  # any input order
+        meta, bs = formats.ef_encode_coords(r[perm], c[perm], H, W, T)
+        m2, b2 = O.ef_encode(mask, T)
+        assert np.array_equal(meta, m2), (H, W, T, d)
+        assert np.array_equal(bs, b2), (H, W, T, d)
+    with pytest.raises(ValueError):
+        formats.ef_encode_coords([1, 1], [2, 2], 4, 4, 4)
