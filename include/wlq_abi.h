@@ -24,8 +24,9 @@
  * passed (lora_h / lora_H, fp32) or, when that pointer is null and lora_A
  * (fp16 [r, K]) is given, computed here as fp32(fp16(x . lora_A^T)) -- the
  * reference caller's F.linear in fp16 followed by .float()
- * (vllm_wlq/linear_method.py:963,984) -- fused into the decode kernel for
- * M <= 32 and r <= 64.
+ * (vllm_wlq/linear_method.py:963,984) -- inside the product kernel for r <= 64
+ * (prepared layout: M <= 128; row layout: M <= 32), else by a separate kernel
+ * before the product.
  *
  * group_size: 0 = one LUT per output row (the reference).  Otherwise a
  * multiple of 32 columns, at least the code window (32/40/64/128 columns for
