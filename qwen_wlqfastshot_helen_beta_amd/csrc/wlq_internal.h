@@ -110,8 +110,9 @@ hipError_t launch_stream(const Layer& L, const void* prepared, int64_t nnz, cons
 // Product for 8 < M <= wide_max_m() on the prepared layout (wlq_wide.hip): activations streamed
 // through LDS slab by slab, outliers overwritten in the dequantized words.
 struct WidePlan {
-  int TB, splits, sps;      // 64-row tile blocks, K splits, 128-column slabs per split
-  int h_kb, h_blocks;       // DoRA column blocks (512 columns) and DoRA blocks (x 32-row chunks of M)
+  int tpw;                  // 16-row W tiles per compute wave (1, or 2 at 128 activation rows)
+  int TB, splits, sps;      // tile blocks (64 tpw rows), K splits, 128-column slabs per split
+  int h_blocks;             // DoRA blocks (each a share of the columns, all activation rows)
   size_t hfin_off, hpart_off, partial_off, workspace_bytes;
   size_t lds;               // dynamic LDS bytes per block
   bool ok;

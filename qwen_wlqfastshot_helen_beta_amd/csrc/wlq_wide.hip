@@ -52,7 +52,6 @@ namespace {
 
 constexpr int kCW = 4;                     // compute waves per block
 constexpr int kThreads = 64 * (kCW + 1);   // + the loader wave
-constexpr int kRows = 16 * kCW;            // W rows per block
 constexpr int kPF = 4;                     // W slabs in flight per compute wave
 constexpr int kPatchCap = 64;              // patches per (slab buffer, compute wave) in LDS
 constexpr int kEpiStride = 72;             // fp16 per LDS row of the epilogue (64 + 8: rows 36 banks apart)
@@ -60,8 +59,7 @@ constexpr int kSc1 = 16;                   // buffer cache-policy bit sc1: devic
 // activation slab buffers by activation rows (the loader runs one fewer slabs ahead)
 constexpr int xbufs(int MB) { return MB <= 16 ? 6 : MB <= 32 ? 4 : 3; }
 constexpr int kMaxSlabs = 127;             // slabs per K split (patch-list starts held in two lane registers)
-constexpr int kHCols = 512;                // columns per DoRA block
-constexpr int kHRows = 32;                 // activation rows per DoRA block
+constexpr int kMaxDoraBlocks = 16;        // DoRA blocks (x.A^T shares) per call
 constexpr int kMaxRank = 64;
 constexpr uint16_t kHalfNaN = 0x7E00u;
 constexpr uint32_t kOutOfRange = 0x80000000u;  // past every buffer resource (sizes < 2^31 bytes)
@@ -85,11 +83,11 @@ struct WideArgs {
   uint32_t g_magic;
   int gshift;
   int splits, sps;          // K splits, slabs per split
-  int h_kb, h_blocks;       // DoRA column blocks and DoRA blocks (h_kb x ceil(M / 32))
-  float* partial;           // [splits][TB][kCW][MB / 16][64] x 4 fp32 (the tiles' register layout)
+  int h_blocks;             // DoRA blocks (x.A^T shares over strided 32-column steps)
+  float* partial;           // [splits][TB][kCW][tiles per wave][MB / 16][64] x 4 fp32 (register layout)
   uint32_t partial_bytes;
   int out_vec;              // 16-byte output stores (N % 8 == 0, out 16-byte aligned)
-  float* hpart;             // [h_kb, M, r]
+  float* hpart;             // [h_blocks, M, r]
   float* hfin;              // [M, r]
   uint32_t* sync;
   uint32_t spin_limit;
@@ -160,41 +158,50 @@ __device__ __forceinline__ void wait_copies(int m) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-// LDS layout of a tile block (bytes).  Main loop:
+// LDS layout of a tile block (bytes), kTiles = kCW x tiles per wave row tiles of 16 rows.
+// Main loop:
 //   [0, XB * MB * 256)           activation slab buffers (MB rows x 16 swizzled units)
-//   lists: [XB][kCW][kPatchCap] u32 patches, headers [XB][64] u32: {start, end} of the
-//          kCW tiles' lists, then zeros (outliers only; one 64-lane copy each)
-//   scratch: [kCW][4 words][64 lanes][8] fp16 dequantized words (outliers only)
+//   lists: [XB][kTiles][kPatchCap] u32 patches, headers [XB][64] u32: {start, end} of the
+//          tiles' lists, then zeros (outliers only; one 64-lane copy each)
+//   scratch: [kTiles][4 words][64 lanes][8] fp16 dequantized words (outliers only)
 // Epilogue (reuses the front): H as fp16 high / low parts, B rows, gamma, the output tile.
-template <int MB, bool CSR>
+// TPW: W row tiles per compute wave; with two, each activation fragment read from LDS feeds
+// two MFMAs (half the LDS traffic per weight) on half as many blocks.
+template <int MB, bool CSR, int TPW_>
 struct WideLds {
   static constexpr int NA = MB / 16;
+  static constexpr int TPW = TPW_;
+  static constexpr int kTiles = kCW * TPW;
+  static constexpr int kBlockRows = 16 * kTiles;
   static constexpr int XB = xbufs(MB);
   static constexpr int kXBytes = XB * MB * 256;
   static constexpr int kListOff = kXBytes;
-  static constexpr int kListBytes = XB * kCW * kPatchCap * 4;
+  static constexpr int kListBytes = XB * kTiles * kPatchCap * 4;
   static constexpr int kHdrOff = kListOff + kListBytes;
   static constexpr int kScratchOff = kHdrOff + XB * 256;
-  static constexpr int kMainBytes = CSR ? kScratchOff + kCW * 64 * 64 : kXBytes;
-  // epilogue: H high / low parts [MB][kEpiStride] fp16, B rows [kRows][kEpiStride], gamma
-  // [kRows], output tile [MB][kEpiStride] fp16
+  static constexpr int kMainBytes = CSR ? kScratchOff + kTiles * 64 * 64 : kXBytes;
+  // epilogue: H high / low parts [MB][kEpiStride] fp16, B rows [kBlockRows][kEpiStride],
+  // gamma [kBlockRows], output tile [MB][kOutStride] fp16 (rows 4 banks apart)
+  static constexpr int kOutStride = kBlockRows + 8;
   static constexpr int kEpiHi = 0;
   static constexpr int kEpiLo = kEpiHi + MB * kEpiStride * 2;
   static constexpr int kEpiB = kEpiLo + MB * kEpiStride * 2;
-  static constexpr int kEpiG = kEpiB + kRows * kEpiStride * 2;
-  static constexpr int kEpiOut = kEpiG + kRows * 2;
-  static constexpr int kEpiBytes = kEpiOut + MB * kEpiStride * 2;
+  static constexpr int kEpiG = kEpiB + kBlockRows * kEpiStride * 2;
+  static constexpr int kEpiOut = kEpiG + kBlockRows * 2;
+  static constexpr int kEpiBytes = kEpiOut + MB * kOutStride * 2;
+  static_assert(2 * kTiles <= 64, "one 64-lane copy holds the header");
 };
 
 // ------------------------------------------------------------------ DoRA blocks
-// hpart[kb, i, j] = sum over columns [512 kb, +512) of x[i, k] * A[j, k] for the block's 32
-// activation rows (waves 0..3, 128 columns each, MFMA 16x16x32); the block that arrives
-// last sums the column blocks in order, rounds H = fp16(sum) and raises the ready slots.
+// hpart[d, i, j] = DoRA block d's share of x[i, :] . A[j, :] for every activation row (NA row
+// groups of 16): wave w takes the 32-column steps d kCW + w, + h_blocks kCW, ... (MFMA
+// 16x16x32), the four wave sums are added through LDS.  The block that arrives last sums the
+// blocks' shares in block order (all of a value's loads in flight at once), rounds
+// H = fp16(sum) and raises the ready slots.  At most kMaxDoraBlocks: while one runs it holds a
+// CU's LDS like a tile block.
+template <int NA>
 __device__ void wide_dora_block(const WideArgs& a, int d, float* red) {
-  constexpr int NA = 2;
   constexpr int JT = kMaxRank / 16;
-  const int kb = d % a.h_kb;
-  const int i0 = (d / a.h_kb) * kHRows;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r16 = lane & 15;
@@ -206,15 +213,14 @@ __device__ void wide_dora_block(const WideArgs& a, int d, float* red) {
     for (int g = 0; g < NA; ++g)
 #pragma unroll
       for (int jt = 0; jt < JT; ++jt) acc[g][jt] = float4_t{0.f, 0.f, 0.f, 0.f};
-    const int kbase = kb * kHCols + wave * 128;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int k = kbase + 32 * ks + 8 * kq;
+    const int nks = (a.K + 31) / 32;
+    for (int ks = d * kCW + wave; ks < nks; ks += a.h_blocks * kCW) {
+      const int k = 32 * ks + 8 * kq;
       const bool kin = k < a.K;  // K % 8 == 0
       u32x4_t xa[NA];
 #pragma unroll
       for (int g = 0; g < NA; ++g) {
-        const int i = i0 + 16 * g + r16;
+        const int i = 16 * g + r16;
         xa[g] = u32x4_t{0u, 0u, 0u, 0u};
         if (i < a.M && kin) xa[g] = *reinterpret_cast<const u32x4_t*>(a.X + (size_t)i * a.K + k);
       }
@@ -245,13 +251,13 @@ __device__ void wide_dora_block(const WideArgs& a, int d, float* red) {
     const int e = (idx >> 6) & 3;
     const int jt = (idx >> 8) % jt_n;
     const int g = (idx >> 8) / jt_n;
-    const int i = i0 + 16 * g + 4 * (ln >> 4) + e;
+    const int i = 16 * g + 4 * (ln >> 4) + e;
     const int j = 16 * jt + (ln & 15);
     if (i < a.M && j < a.r) {
       float v = 0.f;
 #pragma unroll
       for (int w = 0; w < kCW; ++w) v += red[(((w * NA + g) * JT + jt) * 4 + e) * 64 + ln];
-      store_dev(a.hpart + ((size_t)kb * a.M + i) * a.r + j, v);
+      store_dev(a.hpart + ((size_t)d * a.M + i) * a.r + j, v);
     }
   }
   stores_done();
@@ -265,16 +271,15 @@ __device__ void wide_dora_block(const WideArgs& a, int d, float* red) {
   __syncthreads();
   if (!s_last) return;
   compiler_fence();
+  const size_t pstride = (size_t)a.M * a.r;
   for (int idx = threadIdx.x; idx < a.M * a.r; idx += blockDim.x) {
+    float t[kMaxDoraBlocks];
+#pragma unroll
+    for (int u = 0; u < kMaxDoraBlocks; ++u) t[u] = load_dev(a.hpart + (size_t)min(u, a.h_blocks - 1) * pstride + idx);
     float v = 0.f;
-    for (int b0 = 0; b0 < a.h_kb; b0 += 8) {
-      float t[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) t[u] = load_dev(a.hpart + (size_t)min(b0 + u, a.h_kb - 1) * a.M * a.r + idx);
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (b0 + u < a.h_kb) v += t[u];
-    }
+    for (int u = 0; u < kMaxDoraBlocks; ++u)
+      if (u < a.h_blocks) v += t[u];
     store_dev(a.hfin + idx, h2f(f2h_rn(v)));  // the reference's F.linear output is fp16
   }
   stores_done();
@@ -292,18 +297,21 @@ struct Slab {
   u32x4_t lo, hi;
 };
 
-template <int LM, int MB, bool CSR>
+template <int LM, int MB, bool CSR, int TPW_>
 __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
-  using Lds = WideLds<MB, CSR>;
+  using Lds = WideLds<MB, CSR, TPW_>;
   constexpr int NA = Lds::NA;
   constexpr int kDma = MB / 4;  // loader copies per activation slab (1 KB = 4 rows each)
   constexpr int XB = Lds::XB;    // activation slab buffers
   constexpr int XA = XB - 1;     // slabs the loader runs ahead
+  constexpr int TPW = Lds::TPW;  // row tiles per compute wave
+  constexpr int kTiles = Lds::kTiles;
+  constexpr int kBlockRows = Lds::kBlockRows;
   extern __shared__ __align__(16) unsigned char smem[];
 
   int bid = blockIdx.x;
   if (bid < a.h_blocks) {
-    wide_dora_block(a, bid, reinterpret_cast<float*>(smem));
+    wide_dora_block<NA>(a, bid, reinterpret_cast<float*>(smem));
     return;
   }
   bid -= a.h_blocks;
@@ -325,9 +333,11 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
   __shared__ int s_err;  // poison: a failed hand-off (this call or the sticky error word)
   if (threadIdx.x == 0) s_err = 0;  // (ordered before its uses by the first barrier)
 
-  float4_t acc[NA];
+  float4_t acc[TPW][NA];  // compute wave w, tile jt: D rows 16 g + 4 kq + e, column 16 (w TPW + jt) + r
 #pragma unroll
-  for (int g = 0; g < NA; ++g) acc[g] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int jt = 0; jt < TPW; ++jt)
+#pragma unroll
+    for (int g = 0; g < NA; ++g) acc[jt][g] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   // The loader and the compute waves run separate loops with the same number of barriers
   // (one per slab): neither's wait-count bookkeeping sees the other's loads.
@@ -335,7 +345,7 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
     // ------------------------------------------------------------------ loader wave
     // Patch-list starts of the block's tiles for slabs s0 .. s0 + nsl: tile w's start of
     // slab s0 + j is lane j of pa[w] (j < 64) or pb[w] (j >= 64).
-    uint32_t pa[kCW], pb[kCW];
+    uint32_t pa[kTiles], pb[kTiles];
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.X), (short)0, (int)((size_t)a.M * a.K * 2), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
@@ -363,38 +373,38 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
       const int b = j % XB;
       {
         const int w = lane >> 1;
-        const uint32_t off = (lane < 2 * kCW && tb * kCW + w < a.T)
-                                 ? (uint32_t)((((size_t)(tb * kCW + w) * a.S + s0 + j + (lane & 1))) * 4)
+        const uint32_t off = (lane < 2 * kTiles && tb * kTiles + w < a.T)
+                                 ? (uint32_t)((((size_t)(tb * kTiles + w) * a.S + s0 + j + (lane & 1))) * 4)
                                  : kOutOfRange;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(ir, hdr + 64 * b, 4, off, 0, 0, 0);
       }
 #pragma unroll
-      for (int w = 0; w < kCW; ++w) {
+      for (int w = 0; w < kTiles; ++w) {
         const uint32_t st = (uint32_t)__builtin_amdgcn_readlane((int)(j < 64 ? pa[w] : pb[w]), j & 63);
         const uint32_t en = (uint32_t)__builtin_amdgcn_readlane((int)(j + 1 < 64 ? pa[w] : pb[w]), (j + 1) & 63);
-        const int n = tb * kCW + w < a.T ? (int)(en - st) : 0;
+        const int n = tb * kTiles + w < a.T ? (int)(en - st) : 0;
         const uint32_t off = lane < n ? (st + (uint32_t)lane) * 4u : kOutOfRange;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(pr, lists + (b * kCW + w) * kPatchCap, 4, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(pr, lists + (b * kTiles + w) * kPatchCap, 4, off, 0, 0, 0);
       }
     };
-    constexpr int kCopies = kDma + (CSR ? kCW + 1 : 0);
+    constexpr int kCopies = kDma + (CSR ? kTiles + 1 : 0);
     const int npre = min(XA, nsl);
     for (int j = 0; j < npre; ++j) issue_x(j);
     if constexpr (CSR) {
 #pragma unroll
-      for (int w = 0; w < kCW; ++w) {
-        const size_t base = (size_t)min(tb * kCW + w, a.T - 1) * a.S + s0;  // + j <= T * S
+      for (int w = 0; w < kTiles; ++w) {
+        const size_t base = (size_t)min(tb * kTiles + w, a.T - 1) * a.S + s0;  // + j <= T * S
         pa[w] = a.wpidx[base + min(lane, nsl)];
         pb[w] = a.wpidx[base + min(64 + lane, nsl)];
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // (and every activation copy issued so far)
 #pragma unroll
-      for (int w = 0; w < kCW; ++w) {  // plain registers from here on (no load pending on them)
+      for (int w = 0; w < kTiles; ++w) {  // plain registers from here on (no load pending on them)
         asm volatile("v_mov_b32 %0, %1" : "=v"(pa[w]) : "v"(pa[w]));
         asm volatile("v_mov_b32 %0, %1" : "=v"(pb[w]) : "v"(pb[w]));
       }
       for (int j = 0; j < npre; ++j) issue_lists(j);
-      wait_copies<kCW + 1, XA>(npre - 1);  // slab 0's lists in LDS (the later slabs' may be in flight)
+      wait_copies<kTiles + 1, XA>(npre - 1);  // slab 0's lists in LDS (the later slabs' may be in flight)
     } else {
       wait_copies<kCopies, XA>(npre - 1);  // slab 0 in LDS
     }
@@ -412,74 +422,91 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
     }
   } else {
     // ------------------------------------------------------------------ compute waves
-    const int t = min(tb * kCW + wave, a.T - 1);
-    const u32x4_t* qb = a.codes + (size_t)t * a.S * 64 + lane;
-    const u32x4_t* lb = a.planes + (size_t)t * a.ng * 32 + r;
+    // row tiles wt = w TPW + jt of the block (t = tb kTiles + wt), kPFW slabs of each in flight
+    constexpr int kPFW = kPF / TPW;
+    const u32x4_t* qb[TPW];
+    const u32x4_t* lb[TPW];
+#pragma unroll
+    for (int jt = 0; jt < TPW; ++jt) {
+      const int t = min(tb * kTiles + wave * TPW + jt, a.T - 1);
+      qb[jt] = a.codes + (size_t)t * a.S * 64 + lane;
+      lb[jt] = a.planes + (size_t)t * a.ng * 32 + r;
+    }
     auto ld = [](const u32x4_t* p) __attribute__((always_inline)) { return __builtin_nontemporal_load(p); };
-    auto load_slab = [&](Slab& sl, int s) __attribute__((always_inline)) {
-      sl.codes = ld(qb + (size_t)s * 64);
-      if constexpr (LM == 2) {
-        const int g = s >> a.gshift;
-        sl.lo = ld(lb + g * 32);
-        sl.hi = ld(lb + g * 32 + 16);
-      } else if constexpr (LM == 1) {
-        const int g = min(group_of(128 * s + 32 * kq, a.g_magic), a.ng - 1);
-        sl.lo = ld(lb + g * 32);
-        sl.hi = ld(lb + g * 32 + 16);
+    auto load_slab = [&](Slab* sl, int s) __attribute__((always_inline)) {  // sl[TPW]
+#pragma unroll
+      for (int jt = 0; jt < TPW; ++jt) {
+        sl[jt].codes = ld(qb[jt] + (size_t)s * 64);
+        if constexpr (LM == 2) {
+          const int g = s >> a.gshift;
+          sl[jt].lo = ld(lb[jt] + g * 32);
+          sl[jt].hi = ld(lb[jt] + g * 32 + 16);
+        } else if constexpr (LM == 1) {
+          const int g = min(group_of(128 * s + 32 * kq, a.g_magic), a.ng - 1);
+          sl[jt].lo = ld(lb[jt] + g * 32);
+          sl[jt].hi = ld(lb[jt] + g * 32 + 16);
+        }
       }
     };
-    LutPlanes<4> pl;
+    LutPlanes<4> pl[TPW];
     if constexpr (LM == 0) {
-      const u32x4_t lo = lb[0];
-      const u32x4_t hi = lb[16];
-      pl.lo[0] = lo.x; pl.lo[1] = lo.y; pl.lo[2] = lo.z; pl.lo[3] = lo.w;
-      pl.hi[0] = hi.x; pl.hi[1] = hi.y; pl.hi[2] = hi.z; pl.hi[3] = hi.w;
-    }
-    Slab buf[kPF];
 #pragma unroll
-    for (int u = 0; u < kPF; ++u) load_slab(buf[u], s0 + min(u, nsl - 1));
+      for (int jt = 0; jt < TPW; ++jt) {
+        const u32x4_t lo = lb[jt][0];
+        const u32x4_t hi = lb[jt][16];
+        pl[jt].lo[0] = lo.x; pl[jt].lo[1] = lo.y; pl[jt].lo[2] = lo.z; pl[jt].lo[3] = lo.w;
+        pl[jt].hi[0] = hi.x; pl[jt].hi[1] = hi.y; pl[jt].hi[2] = hi.z; pl[jt].hi[3] = hi.w;
+      }
+    }
+    Slab buf[kPFW][TPW];
+#pragma unroll
+    for (int u = 0; u < kPFW; ++u) load_slab(buf[u], s0 + min(u, nsl - 1));
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // s_err initialised
     raw_barrier();
 
-    // scratch [wave][word q][lane][8 fp16]: consecutive lanes at consecutive 16-byte units
-    uint16_t* my_scr = scratch + (wave * 256 + lane) * 8;
-    auto consume = [&](const Slab& sl, int j) __attribute__((always_inline)) {
-      LutPlanes<4> t4;
-      if constexpr (LM == 0) {
-        t4 = pl;
-      } else {
-        t4.lo[0] = sl.lo.x; t4.lo[1] = sl.lo.y; t4.lo[2] = sl.lo.z; t4.lo[3] = sl.lo.w;
-        t4.hi[0] = sl.hi.x; t4.hi[1] = sl.hi.y; t4.hi[2] = sl.hi.z; t4.hi[3] = sl.hi.w;
-      }
-      const uint32_t w[4] = {sl.codes.x, sl.codes.y, sl.codes.z, sl.codes.w};
-      u32x4_t bq[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        uint32_t b[4];
-        dequant_word4s(w[q], t4, b);
-        bq[q] = u32x4_t{b[0], b[1], b[2], b[3]};
-      }
+    auto consume = [&](const Slab* sl, int j) __attribute__((always_inline)) {  // sl[TPW]
       const int b = j % XB;
-      if constexpr (CSR) {
-        // outliers: dequantized words to the wave's scratch, the slab's patches (one per lane),
-        // words back (one wave's LDS operations complete in order)
-        const uint32_t st = hdr[64 * b + 2 * wave];
-        const int n = (int)(hdr[64 * b + 2 * wave + 1] - st);
-        if (n > 0) {
+      u32x4_t bq[TPW][4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4_t*>(my_scr + 512 * q) = bq[q];
-          auto apply = [&](uint32_t p) __attribute__((always_inline)) {  // element e of lane l: word e / 8
-            const uint32_t e = (p >> 6) & 31u;
-            scratch[((wave * 4 + (e >> 3)) * 64 + (p & 63u)) * 8 + (e & 7u)] = (uint16_t)((p >> 24) << 8);
-          };
-          if (lane < n) apply(lists[(b * kCW + wave) * kPatchCap + lane]);
-          if (n > kPatchCap) {  // the rest from global memory (rare: > 64 outliers in 16 x 128 weights)
-            const uint32_t np = a.patch_bytes >> 2;
-            for (int e = kPatchCap + lane; e < n; e += 64)
-              if (st + (uint32_t)e < np) apply(a.wpatch[st + e]);
+      for (int jt = 0; jt < TPW; ++jt) {
+        LutPlanes<4> t4;
+        if constexpr (LM == 0) {
+          t4 = pl[jt];
+        } else {
+          t4.lo[0] = sl[jt].lo.x; t4.lo[1] = sl[jt].lo.y; t4.lo[2] = sl[jt].lo.z; t4.lo[3] = sl[jt].lo.w;
+          t4.hi[0] = sl[jt].hi.x; t4.hi[1] = sl[jt].hi.y; t4.hi[2] = sl[jt].hi.z; t4.hi[3] = sl[jt].hi.w;
+        }
+        const uint32_t w[4] = {sl[jt].codes.x, sl[jt].codes.y, sl[jt].codes.z, sl[jt].codes.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t bv[4];
+          dequant_word4s(w[q], t4, bv);
+          bq[jt][q] = u32x4_t{bv[0], bv[1], bv[2], bv[3]};
+        }
+        if constexpr (CSR) {
+          // outliers: dequantized words to the tile's scratch [word q][lane][8 fp16] (consecutive
+          // lanes at consecutive 16-byte units), the slab's patches (one per lane), words back
+          // (one wave's LDS operations complete in order)
+          const int wt = wave * TPW + jt;
+          const uint32_t st = hdr[64 * b + 2 * wt];
+          const int n = (int)(hdr[64 * b + 2 * wt + 1] - st);
+          if (n > 0) {
+            uint16_t* scr = scratch + wt * 2048;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) *reinterpret_cast<u32x4_t*>(scr + (q * 64 + lane) * 8) = bq[jt][q];
+            auto apply = [&](uint32_t p) __attribute__((always_inline)) {  // element e of lane l: word e / 8
+              const uint32_t e = (p >> 6) & 31u;
+              scr[((e >> 3) * 64 + (p & 63u)) * 8 + (e & 7u)] = (uint16_t)((p >> 24) << 8);
+            };
+            if (lane < n) apply(lists[(b * kTiles + wt) * kPatchCap + lane]);
+            if (n > kPatchCap) {  // the rest from global memory (rare: > 64 outliers in 16 x 128 weights)
+              const uint32_t np = a.patch_bytes >> 2;
+              for (int e = kPatchCap + lane; e < n; e += 64)
+                if (st + (uint32_t)e < np) apply(a.wpatch[st + e]);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) bq[jt][q] = *reinterpret_cast<const u32x4_t*>(scr + (q * 64 + lane) * 8);
           }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) bq[q] = *reinterpret_cast<const u32x4_t*>(my_scr + 512 * q);
         }
       }
       const unsigned char* xb = xbase + b * (MB * 256);
@@ -489,7 +516,8 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
 #pragma unroll
         for (int g = 0; g < NA; ++g) {
           const u32x4_t av = *reinterpret_cast<const u32x4_t*>(xb + (16 * g + r) * 256 + v);
-          acc[g] = mfma16x16x32(av, bq[q], acc[g]);
+#pragma unroll
+          for (int jt = 0; jt < TPW; ++jt) acc[jt][g] = mfma16x16x32(av, bq[jt][q], acc[jt][g]);
         }
       }
       // this slab's LDS reads are complete before the barrier lets the loader refill the buffer
@@ -497,52 +525,55 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
       raw_barrier();
     };
 
-    // Steady state: every slot consumed is reloaded kPF slabs ahead; then one round with
+    // Steady state: every slot consumed is reloaded kPFW slabs ahead; then one round with
     // conditional reloads and a last round without (nsl is block-uniform).
     int j0 = 0;
-    for (; j0 + 2 * kPF <= nsl; j0 += kPF) {
+    for (; j0 + 2 * kPFW <= nsl; j0 += kPFW) {
 #pragma unroll
-      for (int u = 0; u < kPF; ++u) {
+      for (int u = 0; u < kPFW; ++u) {
         consume(buf[u], j0 + u);
-        load_slab(buf[u], s0 + j0 + u + kPF);
+        load_slab(buf[u], s0 + j0 + u + kPFW);
         __builtin_amdgcn_sched_barrier(0);  // keep each reload right behind its slot's use
       }
     }
     if (j0 < nsl) {
 #pragma unroll
-      for (int u = 0; u < kPF; ++u) {
+      for (int u = 0; u < kPFW; ++u) {
         if (j0 + u < nsl) {
           consume(buf[u], j0 + u);
-          if (j0 + u + kPF < nsl) load_slab(buf[u], s0 + j0 + u + kPF);
+          if (j0 + u + kPFW < nsl) load_slab(buf[u], s0 + j0 + u + kPFW);
         }
       }
-      j0 += kPF;
+      j0 += kPFW;
 #pragma unroll
-      for (int u = 0; u < kPF; ++u)
+      for (int u = 0; u < kPFW; ++u)
         if (j0 + u < nsl) consume(buf[u], j0 + u);
     }
   }
 
   // ---------------------------------------------------------------- completion
-  // Compute wave w holds D[i = 16 g + 4 kq + e][block column 16 w + r] in acc[g][e]; the
-  // epilogue works on that register layout (the LDS of the main loop is reused below).
+  // Compute wave w holds D[i = 16 g + 4 kq + e][block column 16 (w TPW + jt) + r] in
+  // acc[jt][g][e]; the epilogue works on that register layout (the main loop's LDS is reused).
   __syncthreads();
   const int slots = min(a.TB, kMaxSlots);
   uint32_t* slot = a.sync + kSyncSlot0 + kSlotWords * (tb % slots);
   const bool h_fused = a.r > 0 && a.h_blocks > 0;
   uint32_t err = 0u;
   if (a.splits > 1) {
-    // Split partials in the register layout, [split][tile block][wave][g][lane] x 4 fp32,
+    // Split partials in the register layout, [split][tile block][wave][jt][g][lane] x 4 fp32,
     // with 16-byte device-coherent (sc1) stores and loads.
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(a.partial, (short)0, (int)a.partial_bytes,
                                                                          kRsrcWord3);
-    auto poff = [&](int sp, int g) __attribute__((always_inline)) {
-      return (int)((((((size_t)sp * a.TB + tb) * kCW + wave) * NA + g) * 64 + lane) * 16);
+    auto poff = [&](int sp, int jt, int g) __attribute__((always_inline)) {
+      return (int)(((((((size_t)sp * a.TB + tb) * kCW + wave) * TPW + jt) * NA + g) * 64 + lane) * 16);
     };
     if (!loader) {
 #pragma unroll
-      for (int g = 0; g < NA; ++g)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[g]), prs, poff(split, g), 0, kSc1);
+      for (int jt = 0; jt < TPW; ++jt)
+#pragma unroll
+        for (int g = 0; g < NA; ++g)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, acc[jt][g]), prs, poff(split, jt, g), 0,
+                                                 kSc1);
     }
     stores_done();
     __syncthreads();
@@ -565,21 +596,29 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
     if (!loader) {
       // the splits' partials summed in split order (the same sum whichever block is last),
       // kU splits' loads in flight at a time
-      constexpr int kU = NA >= 8 ? 2 : NA >= 4 ? 4 : 8;
+      constexpr int kNV = TPW * NA;
+      constexpr int kU = kNV >= 8 ? 2 : kNV >= 4 ? 4 : 8;
 #pragma unroll
-      for (int g = 0; g < NA; ++g) acc[g] = float4_t{0.f, 0.f, 0.f, 0.f};
+      for (int jt = 0; jt < TPW; ++jt)
+#pragma unroll
+        for (int g = 0; g < NA; ++g) acc[jt][g] = float4_t{0.f, 0.f, 0.f, 0.f};
       for (int sp0 = 0; sp0 < a.splits; sp0 += kU) {
-        u32x4_t v[kU][NA];
+        u32x4_t v[kU][TPW][NA];
 #pragma unroll
         for (int u = 0; u < kU; ++u)
 #pragma unroll
-          for (int g = 0; g < NA; ++g)
-            v[u][g] = __builtin_amdgcn_raw_buffer_load_b128(prs, poff(min(sp0 + u, a.splits - 1), g), 0, kSc1);
+          for (int jt = 0; jt < TPW; ++jt)
+#pragma unroll
+            for (int g = 0; g < NA; ++g)
+              v[u][jt][g] =
+                  __builtin_amdgcn_raw_buffer_load_b128(prs, poff(min(sp0 + u, a.splits - 1), jt, g), 0, kSc1);
 #pragma unroll
         for (int u = 0; u < kU; ++u)
           if (sp0 + u < a.splits)
 #pragma unroll
-            for (int g = 0; g < NA; ++g) acc[g] += __builtin_bit_cast(float4_t, v[u][g]);
+            for (int jt = 0; jt < TPW; ++jt)
+#pragma unroll
+              for (int g = 0; g < NA; ++g) acc[jt][g] += __builtin_bit_cast(float4_t, v[u][jt][g]);
       }
     }
   }
@@ -617,15 +656,15 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
     for (int idx = threadIdx.x; idx < a.M * a.r; idx += kThreads)
       hmax = max(hmax, __float_as_uint(hsrc[idx]) & 0x7FFFFFFFu);  // (NaN bit patterns order above inf)
     if (hmax != 0u) atomicMax(&s_hmax, hmax);
-    for (int u = threadIdx.x; u < kRows * (rp / 8); u += kThreads) {  // B rows, zero beyond rank r
+    for (int u = threadIdx.x; u < kBlockRows * (rp / 8); u += kThreads) {  // B rows, zero beyond rank r
       const int row = u / (rp / 8);
       const int c8 = 8 * (u % (rp / 8));
-      const int n = min(tb * kRows + row, a.N - 1);
+      const int n = min(tb * kBlockRows + row, a.N - 1);
       u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
       if (c8 < a.r) v = *reinterpret_cast<const u32x4_t*>(a.B + (size_t)n * a.r + c8);
       *reinterpret_cast<u32x4_t*>(b_s + row * kEpiStride + c8) = v;
     }
-    if (threadIdx.x < kRows) g_s[threadIdx.x] = a.gamma[min(tb * kRows + (int)threadIdx.x, a.N - 1)];
+    if (threadIdx.x < kBlockRows) g_s[threadIdx.x] = a.gamma[min(tb * kBlockRows + (int)threadIdx.x, a.N - 1)];
     __syncthreads();
     const int hex = (int)((s_hmax >> 23) & 0xFFu) - 127;  // max |H| < 2^(hex + 1)
     const int sh = max(0, hex - 14);                     // 2^-sh max |H| < 2^15
@@ -639,24 +678,28 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
     }
     __syncthreads();
     if (!loader) {
-      float4_t dd[NA];
-#pragma unroll
-      for (int g = 0; g < NA; ++g) dd[g] = float4_t{0.f, 0.f, 0.f, 0.f};
-      for (int kk = 0; kk < rp; kk += 32) {
-        const u32x4_t bb = *reinterpret_cast<const u32x4_t*>(b_s + (16 * wave + r) * kEpiStride + kk + 8 * kq);
-#pragma unroll
-        for (int g = 0; g < NA; ++g) {
-          const int ro = (16 * g + r) * kEpiStride + kk + 8 * kq;
-          dd[g] = mfma16x16x32(*reinterpret_cast<const u32x4_t*>(h_hi + ro), bb, dd[g]);
-          dd[g] = mfma16x16x32(*reinterpret_cast<const u32x4_t*>(h_lo + ro), bb, dd[g]);
-        }
-      }
       const float sc = ldexpf(a.scale, sh);
-      const float gam = h2f(g_s[16 * wave + r]);
 #pragma unroll
-      for (int g = 0; g < NA; ++g)
+      for (int jt = 0; jt < TPW; ++jt) {
+        const int col = 16 * (wave * TPW + jt) + r;  // block column of this lane's outputs
+        float4_t dd[NA];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[g][e] = (acc[g][e] + sc * dd[g][e]) * gam;
+        for (int g = 0; g < NA; ++g) dd[g] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int kk = 0; kk < rp; kk += 32) {
+          const u32x4_t bb = *reinterpret_cast<const u32x4_t*>(b_s + col * kEpiStride + kk + 8 * kq);
+#pragma unroll
+          for (int g = 0; g < NA; ++g) {
+            const int ro = (16 * g + r) * kEpiStride + kk + 8 * kq;
+            dd[g] = mfma16x16x32(*reinterpret_cast<const u32x4_t*>(h_hi + ro), bb, dd[g]);
+            dd[g] = mfma16x16x32(*reinterpret_cast<const u32x4_t*>(h_lo + ro), bb, dd[g]);
+          }
+        }
+        const float gam = h2f(g_s[col]);
+#pragma unroll
+        for (int g = 0; g < NA; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[jt][g][e] = (acc[jt][g][e] + sc * dd[g][e]) * gam;
+      }
     }
   }
   if (err != 0u) s_err = 1;
@@ -665,21 +708,25 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
     cons_old = atomicAdd(slot + 1, 1u);
     counted = true;
   }
-  // outputs: fp16 through LDS ([MB][kEpiStride]), then rows of 64 columns in 16-byte stores
+  // outputs: fp16 through LDS ([MB][kOutStride]), then rows of kBlockRows columns in 16-byte stores
   const bool poisoned = s_err != 0;
   if (!loader) {
 #pragma unroll
-    for (int g = 0; g < NA; ++g)
+    for (int jt = 0; jt < TPW; ++jt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        o_s[(16 * g + 4 * kq + e) * kEpiStride + 16 * wave + r] = poisoned ? kHalfNaN : f2h_rn(acc[g][e]);
+      for (int g = 0; g < NA; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o_s[(16 * g + 4 * kq + e) * Lds::kOutStride + 16 * (wave * TPW + jt) + r] =
+              poisoned ? kHalfNaN : f2h_rn(acc[jt][g][e]);
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < a.M * 8; idx += kThreads) {
-    const int i = idx >> 3;
-    const int c8 = 8 * (idx & 7);
-    const int n0 = tb * kRows + c8;
-    const uint16_t* src = o_s + i * kEpiStride + c8;
+  constexpr int kUnits = kBlockRows / 8;  // 16-byte units per output row of the block
+  for (int idx = threadIdx.x; idx < a.M * kUnits; idx += kThreads) {
+    const int i = idx / kUnits;
+    const int c8 = 8 * (idx - i * kUnits);
+    const int n0 = tb * kBlockRows + c8;
+    const uint16_t* src = o_s + i * Lds::kOutStride + c8;
     uint16_t* dst = a.out + (size_t)i * a.N + n0;
     if (a.out_vec && n0 + 8 <= a.N) {
       *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
@@ -699,9 +746,9 @@ __global__ __launch_bounds__(kThreads) void wide_kernel(const WideArgs a) {
   }
 }
 
-template <int LM, int MB, bool CSR>
+template <int LM, int MB, bool CSR, int TPW>
 hipError_t launch_wide_tpl(const WideArgs& a, dim3 grid, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((wide_kernel<LM, MB, CSR>), grid, dim3(kThreads), lds, stream, a);
+  hipLaunchKernelGGL((wide_kernel<LM, MB, CSR, TPW>), grid, dim3(kThreads), lds, stream, a);
   return hipGetLastError();
 }
 
@@ -709,18 +756,19 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 int wide_mb(int M) { return M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128; }
 
-template <int MB>
+template <int MB, int TPW>
 size_t wide_lds_bytes(bool csr) {
-  const size_t main = csr ? (size_t)WideLds<MB, true>::kMainBytes : (size_t)WideLds<MB, false>::kMainBytes;
-  return std::max(main, (size_t)WideLds<MB, true>::kEpiBytes);
+  const size_t main =
+      csr ? (size_t)WideLds<MB, true, TPW>::kMainBytes : (size_t)WideLds<MB, false, TPW>::kMainBytes;
+  return std::max(main, (size_t)WideLds<MB, true, TPW>::kEpiBytes);
 }
 
-size_t wide_lds(int M, bool csr) {
+size_t wide_lds(int M, bool csr, int tpw) {
   switch (wide_mb(M)) {
-    case 16: return wide_lds_bytes<16>(csr);
-    case 32: return wide_lds_bytes<32>(csr);
-    case 64: return wide_lds_bytes<64>(csr);
-    default: return wide_lds_bytes<128>(csr);
+    case 16: return wide_lds_bytes<16, 1>(csr);
+    case 32: return wide_lds_bytes<32, 1>(csr);
+    case 64: return wide_lds_bytes<64, 1>(csr);
+    default: return tpw == 2 ? wide_lds_bytes<128, 2>(csr) : wide_lds_bytes<128, 1>(csr);
   }
 }
 
@@ -732,9 +780,16 @@ WidePlan plan_wide(int N, int K, int M, int cu_count, int rank, int fused_rank, 
   WidePlan p{};
   const int T = (N + 15) / 16;
   const int S = (K + 127) / 128;
-  p.TB = (T + kCW - 1) / kCW;
-  p.lds = wide_lds(M, csr);
-  if (fused_rank > 0) p.lds = std::max<size_t>(p.lds, 2 * (kMaxRank / 16) * 4 * 64 * kCW * 4);  // DoRA blocks' sums
+  // two row tiles per compute wave at 128 activation rows on layers wide enough to keep the CUs
+  // busy with half the blocks or long enough in K to split (measured: gate 18944x3584 at M = 128
+  // 106 -> 67 us, down 3584x18944 73 -> 66 us; q/k/v and every M <= 64 slower)
+  const int cus = std::max(1, cu_count);
+  p.tpw = (wide_mb(M) == 128 && ((T + 2 * kCW - 1) / (2 * kCW) >= cus / 2 || S >= 64)) ? 2 : 1;
+  const int tiles = kCW * p.tpw;  // row tiles per block
+  p.TB = (T + tiles - 1) / tiles;
+  p.lds = wide_lds(M, csr, p.tpw);
+  if (fused_rank > 0)  // the DoRA blocks' wave sums, [kCW][row groups][kMaxRank / 16][4][64] fp32
+    p.lds = std::max<size_t>(p.lds, (size_t)kCW * (wide_mb(M) / 16) * (kMaxRank / 16) * 4 * 64 * 4);
   p.ok = M > 8 && M <= wide_max_m() && (chunk == 512 || chunk == 640) && rank % 8 == 0 && rank <= kMaxRank &&
          fused_rank % 8 == 0 && fused_rank <= kMaxRank && p.lds <= 160 * 1024;
   if (!p.ok) return p;
@@ -744,20 +799,21 @@ WidePlan plan_wide(int N, int K, int M, int cu_count, int rank, int fused_rank, 
   // shorter than ~7 slabs spends more in its prologue and hand-off than it gains, except
   // on layers too narrow to occupy a quarter of the CUs (k/v: 8 tile blocks), where 4
   // slabs per split measured best.
-  const int cus = std::max(1, cu_count);
+  // The DoRA blocks are dispatched first and hold CU slots too: a tile block past the cap waits
+  // for a second round (down 3584x18944 at M = 128: 8 splits 62 us, 9 splits 75 us).
   const int min_slabs = p.TB < cus / 4 ? 4 : 7;
-  const int cap = M <= 16 ? cus * 5 / 2 : M <= 64 ? 2 * cus : cus;
+  const int cap = (M <= 16 ? cus * 5 / 2 : M <= 64 ? 2 * cus : cus) -
+                  (fused_rank > 0 ? std::min(kMaxDoraBlocks, (K + 511) / 512) : 0);
   const int smin = (S + kMaxSlabs - 1) / kMaxSlabs;
   int splits = std::max(smin, std::min(cap / p.TB, S / min_slabs));
   const int sps = (S + splits - 1) / splits;
   splits = (S + sps - 1) / sps;
   p.splits = splits;
   p.sps = sps;
-  p.h_kb = fused_rank > 0 ? (K + kHCols - 1) / kHCols : 0;
-  p.h_blocks = fused_rank > 0 ? p.h_kb * ((M + kHRows - 1) / kHRows) : 0;
+  p.h_blocks = fused_rank > 0 ? std::min(kMaxDoraBlocks, (K + 511) / 512) : 0;
   const size_t hf = fused_rank > 0 ? align256((size_t)M * fused_rank * 4) : 0;
-  const size_t hp = fused_rank > 0 ? align256((size_t)p.h_kb * M * fused_rank * 4) : 0;
-  const size_t part = splits > 1 ? (size_t)splits * p.TB * kRows * wide_mb(M) * 4 : 0;
+  const size_t hp = fused_rank > 0 ? align256((size_t)p.h_blocks * M * fused_rank * 4) : 0;
+  const size_t part = splits > 1 ? (size_t)splits * p.TB * 16 * tiles * wide_mb(M) * 4 : 0;
   p.hfin_off = 0;
   p.hpart_off = hf;
   p.partial_off = hf + hp;
@@ -797,7 +853,6 @@ hipError_t launch_wide(const Layer& L, const void* prepared, int64_t nnz, const 
   a.splits = plan.splits;
   a.sps = plan.sps;
   const bool fused_h = D.r > 0 && D.H == nullptr;
-  a.h_kb = fused_h ? plan.h_kb : 0;
   a.h_blocks = fused_h ? plan.h_blocks : 0;
   char* ws = reinterpret_cast<char*>(workspace);
   a.hfin = reinterpret_cast<float*>(ws + plan.hfin_off);
@@ -817,12 +872,14 @@ hipError_t launch_wide(const Layer& L, const void* prepared, int64_t nnz, const 
   const dim3 grid(a.h_blocks + plan.TB * plan.splits);
   const size_t lds = plan.lds;
   const int mb = wide_mb(M);
-#define WLQ_WIDE_MB(LMV, CSRV)                                                   \
-  switch (mb) {                                                                 \
-    case 16: return launch_wide_tpl<LMV, 16, CSRV>(a, grid, lds, stream);       \
-    case 32: return launch_wide_tpl<LMV, 32, CSRV>(a, grid, lds, stream);       \
-    case 64: return launch_wide_tpl<LMV, 64, CSRV>(a, grid, lds, stream);       \
-    default: return launch_wide_tpl<LMV, 128, CSRV>(a, grid, lds, stream);      \
+#define WLQ_WIDE_MB(LMV, CSRV)                                                                  \
+  switch (mb) {                                                                                \
+    case 16: return launch_wide_tpl<LMV, 16, CSRV, 1>(a, grid, lds, stream);                   \
+    case 32: return launch_wide_tpl<LMV, 32, CSRV, 1>(a, grid, lds, stream);                   \
+    case 64: return launch_wide_tpl<LMV, 64, CSRV, 1>(a, grid, lds, stream);                   \
+    default:                                                                                   \
+      return plan.tpw == 2 ? launch_wide_tpl<LMV, 128, CSRV, 2>(a, grid, lds, stream)          \
+                           : launch_wide_tpl<LMV, 128, CSRV, 1>(a, grid, lds, stream);         \
   }
 #define WLQ_WIDE_LM(LMV) \
   if (csr) {             \

@@ -198,3 +198,18 @@ def test_wide_given_h_fp32(vw, scale):
             assert np.max(np.abs(yy - rr)) <= 2e-3 * np.max(np.abs(rr)) + 1e-6, f"M={M} scale={scale}"
         else:
             check_close(y, ref, what=f"given fp32 H M={M}")
+
+
+@pytest.mark.parametrize("M", [65, 128])
+def test_wide_two_tiles_per_wave(vw, M):
+    """128-row activation buffers on a layer long in K (65 slabs) run two 16-row W tiles per
+    compute wave (128-row blocks); N = 136 leaves the second block with one tile.  Every LUT
+    mode, DoRA fused / given / off, 3-bit, and 20% outliers (lists beyond the LDS list)."""
+    cases = [(4, gs, dora, 0.01) for gs in (0, 64, 128, 384) for dora in ("fused", "h", "none")]
+    cases += [(3, 128, "fused", 0.01), (4, 128, "fused", 0.2)]
+    for bits, gs, dora, d in cases:
+        _case(M=M, bits=bits, gs=gs, dora=dora, density=d)
+        L = synth.make_layer(N=136, K=8320, bits=bits, group_size=gs, rank=16, density=d, seed=M + gs + bits)
+        x = synth.make_activations(M, L.K, seed=M + 3)
+        y, H = run_prepared(vw, L, x, dora=dora)
+        _check(y, L, x, H, f"two tiles M={M} bits={bits} gs={gs} dora={dora} d={d}")
