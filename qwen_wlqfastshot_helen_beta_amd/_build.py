@@ -28,7 +28,8 @@ ARCH = "gfx950"
 LIB_PATH = os.path.join(PKG, "libwlq_hip.so")
 EXT_DIR = os.path.join(PKG, "vllm_wlq")
 
-HIP_SOURCES = ["wlq_abi.hip", "wlq_skinny.hip", "wlq_stream.hip", "wlq_wide.hip", "wlq_gemm.hip", "wlq_dequant.hip",
+HIP_SOURCES = ["wlq_abi.hip", "wlq_skinny.hip", "wlq_stream.hip", "wlq_wide.hip", "wlq_prefill.hip", "wlq_gemm.hip",
+               "wlq_dequant.hip",
                "wlq_epilogue.hip"]
 HOST_SOURCES = ["wlq_host.cpp"]
 

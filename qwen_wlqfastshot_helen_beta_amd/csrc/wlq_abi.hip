@@ -50,6 +50,12 @@ bool withhold_h() {
   return e != nullptr && e[0] == '1';
 }
 
+bool force_prefill() {
+  if (!hooks_on()) return false;
+  const char* e = std::getenv("WLQ_TEST_FORCE_PREFILL");
+  return e != nullptr && e[0] == '1';
+}
+
 }  // namespace wlq
 
 namespace {
@@ -244,7 +250,8 @@ int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c
   if (st != WLQ_OK) return st;
   const wlq::Dora D = make_dora(lora_B, lora_H, dora_gamma, lora_A, lora_scale, r);
   const bool wide = M > kWideMinM && M <= wlq::wide_max_m();
-  if (prepared != nullptr && M >= 1 && (M <= wlq::stream_max_m() || wide) && L.N > 0 && X != nullptr &&
+  const bool prefill = M >= wlq::prefill_min_m();
+  if (prepared != nullptr && M >= 1 && (M <= wlq::stream_max_m() || wide || prefill) && L.N > 0 && X != nullptr &&
       out != nullptr && wlq::prepared_supported(L.N, L.K, L.bits, L.group_size) && nnz >= 0 &&
       (L.offsets != nullptr || nnz == 0)) {
     const size_t need = wlq::prepared_layout(L.N, L.K, L.group_size, nnz).bytes;
@@ -260,6 +267,27 @@ int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c
     const bool aligned = (reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (reinterpret_cast<uintptr_t>(prepared) & 255u) == 0 &&
                          (!fused_h || (reinterpret_cast<uintptr_t>(D.A) & 15u) == 0) && dora_ok;
     const size_t ws = workspace != nullptr ? workspace_bytes : 0;
+    if (prefill) {
+      const wlq::PrefillPlan p = wlq::plan_prefill(L.N, L.K, (int)M, L.group_size, current_cu_count(), D.r,
+                                                   fused_h ? D.r : 0, L.chunk);
+      const bool need_sync = p.splits > 1 || fused_h;
+      const bool ws_ok = !need_sync || ws >= wlq::kSyncBytes + p.workspace_bytes;
+      const bool runs = p.ok && aligned && (p.preferred || wlq::force_prefill());
+      if (runs && !ws_ok && strict) {
+        wlq::set_error("%s: M=%lld N=%lld K=%lld needs %zu bytes of scratch, more than the %zu bytes it holds", fn,
+                       (long long)M, (long long)N, (long long)K, wlq::kSyncBytes + p.workspace_bytes, ws);
+        return WLQ_ERR_CAPACITY;
+      }
+      if (runs && ws_ok) {
+        char* wbase = reinterpret_cast<char*>(workspace);
+        uint32_t* sync = need_sync ? reinterpret_cast<uint32_t*>(wbase) : nullptr;
+        float* w = need_sync ? reinterpret_cast<float*>(wbase + wlq::kSyncBytes) : nullptr;
+        return hip_status(wlq::launch_prefill(L, prepared, nnz, D, reinterpret_cast<const uint16_t*>(X),
+                                              reinterpret_cast<uint16_t*>(out), (int)M, p, w, sync, stream),
+                          fn);
+      }
+      return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, fn);
+    }
     if (wide) {
       const bool csr = L.offsets != nullptr && nnz > 0;
       const wlq::WidePlan p =
@@ -388,6 +416,11 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
     const int rr = r > 0 && r <= wlq::stream_max_rank() ? r : 0;
     const wlq::WidePlan wp = wlq::plan_wide((int)N, (int)K, (int)M, cus, rr, rr, L.chunk, true);
     need = std::max(need, wp.workspace_bytes + 256);
+  }
+  if (M >= wlq::prefill_min_m() && (bits == 4 || bits == 3)) {  // or the prefill kernel
+    const int rr = r > 0 && r <= wlq::stream_max_rank() ? r : 0;
+    const wlq::PrefillPlan pp = wlq::plan_prefill((int)N, (int)K, (int)M, 0, cus, rr, rr, L.chunk);
+    if (pp.ok) need = std::max(need, pp.workspace_bytes + 256);
   }
   return need > 0 ? wlq::kSyncBytes + need : 0;
 }

@@ -67,6 +67,9 @@ constexpr uint32_t kDefaultSpinLimit = 1u << 24;  // ~1 s of polls
 // product (WLQ_SPIN_LIMIT, WLQ_TEST_WITHHOLD_H, read on every call then).
 uint32_t spin_limit();
 bool withhold_h();
+// Test hook (WLQ_TEST_FORCE_PREFILL=1 with the hooks on): M > 128 products on a prepared layer take
+// the prefill kernel wherever it can run, not only where it is the faster choice.
+bool force_prefill();
 
 int slab_cols(int bits);             // columns one 16-row wave tile covers per step
 int skinny_max_m();
@@ -123,6 +126,25 @@ WidePlan plan_wide(int N, int K, int M, int cu_count, int rank, int fused_rank, 
 hipError_t launch_wide(const Layer& L, const void* prepared, int64_t nnz, const Dora& D, const uint16_t* x,
                        uint16_t* out, int M, const WidePlan& plan, float* workspace, uint32_t* sync,
                        hipStream_t stream);
+
+// Product for M >= prefill_min_m() on the prepared layout (wlq_prefill.hip): W dequantized in
+// registers into 32x32x16 MFMA operands, activations double-buffered through LDS, block tiles of
+// 128 activation rows x 256 W rows.  Per-row LUTs or LUT groups of 128 << g columns.
+struct PrefillPlan {
+  int nblk, mblk, tiles;    // W blocks (256 rows), activation blocks (128 rows), output tiles
+  int splits, sps;          // K splits, 128-column slabs per split
+  int hk, h_blocks;         // DoRA shares per activation block, DoRA blocks
+  int per_xcd, grid;        // tile blocks per XCD, grid size
+  size_t hfin_off, hpart_off, partial_off, workspace_bytes;
+  size_t lds;
+  bool ok;                  // the kernel can run the product
+  bool preferred;           // ... and is the faster choice (measured; otherwise the MFMA GEMM)
+};
+int prefill_min_m();
+PrefillPlan plan_prefill(int N, int K, int M, int group_size, int cu_count, int rank, int fused_rank, int chunk);
+hipError_t launch_prefill(const Layer& L, const void* prepared, int64_t nnz, const Dora& D, const uint16_t* x,
+                          uint16_t* out, int M, const PrefillPlan& plan, float* workspace, uint32_t* sync,
+                          hipStream_t stream);
 
 // out = fp16_rn(sum of fp32 split-K partials [splits, M, N]) (epilogue already applied).
 hipError_t launch_splitk_sum(const float* partial, int splits, int M, int N, uint16_t* out, hipStream_t stream);

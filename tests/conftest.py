@@ -7,6 +7,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
+# The library reads WLQ_TEST_HOOKS once, at its first product: on for the whole test process, so
+# a test may set a hook's variable (WLQ_TEST_FORCE_PREFILL, ...) for its own calls.  With none of
+# them set the products run exactly as without the hooks.
+os.environ.setdefault("WLQ_TEST_HOOKS", "1")
+
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (ROCm) GPU; run with -m gpu")
