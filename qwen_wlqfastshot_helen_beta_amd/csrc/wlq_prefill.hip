@@ -6,13 +6,16 @@
 // (csrc/gemm_kernel.cu:204-228): W0 expanded through the LUTs, outlier positions overwritten
 // by fp16(e5m2 << 8), y = fp16((X.W0^T + s * H.B^T) * gamma) with H = fp16(X.A^T).
 //
-// Design.  W never goes through LDS.  Block tile = 128 activation rows x 256 W rows, four
-// waves (one per SIMD), wave w owning W rows 64 w .. 64 w + 63 of the block as two 32-row
-// pairs.  Per 128-column slab a wave loads its pairs' codes straight from the prepared layout
-// (each lane two 16-byte loads per pair), dequantizes them in registers (dequant_word4s) into
-// the B operands of V_MFMA_F32_32X32X16_F16 and multiplies them with the four 32-row groups of
-// the activation slab, read from LDS as the A operands: each A fragment feeds two MFMAs, each
-// dequantized W word 4 x 32 activation rows.
+// Design.  W never goes through LDS.  Block tile = 128 activation rows x 256 W rows, eight
+// waves (two per SIMD), wave w owning W rows 32 w .. 32 w + 31 of the block (one 32-row pair).
+// Per 128-column slab a wave loads its pair's codes straight from the prepared layout (each lane
+// two 16-byte loads), dequantizes them in registers (dequant_word4s) into the B operands of
+// V_MFMA_F32_32X32X16_F16 and multiplies them with the four 32-row groups of the activation
+// slab, read from LDS as the A operands: each dequantized W word feeds 4 x 32 activation rows.
+// An MFMA holds its own wave's issue for most of its duration, so a wave's lookups and its MFMAs
+// serialize; the second wave on the SIMD fills that time (measured: one wave per SIMD with two
+// pairs each ran gate_proj at M = 2048 in 372 us, two waves with one pair each in 321 us).
+// The dequant of half a slab runs beside the MFMAs of the other half (half-slab pipeline).
 //
 // Operand order.  The prepared layout holds a 16-row tile's slab in the lane order of the
 // 16x16x32 MFMA: lane L = r + 16 kq, word q covers columns 32 kq + 8 q .. +7 of row r.  For
@@ -22,22 +25,22 @@
 // word) is used exactly once per slab; A and B agree on the column of every product.
 //
 // Activations: double-buffered 128-row slabs in LDS (16-byte units XOR-swizzled by row so the
-// 32 rows of a fragment read hit distinct banks), loaded by all 256 threads into registers
+// 32 rows of a fragment read hit distinct banks), loaded by all 512 threads into registers
 // one slab ahead and written at the top of the next iteration; rows >= M and columns >= K
 // read as zeros through the buffer range check.  One barrier per slab.
 //
-// Outliers: the prepared patch lists per (16-row tile, slab).  A wave whose pair has patches
-// in the slab writes its dequantized words to a wave-private LDS scratch in the source-lane
-// order of the prepared layout, applies the patches (one per lane and tile; longer lists
-// continue from global memory) and reads the words back.
+// Outliers: the prepared patch lists per (16-row tile, slab).  A wave writes its dequantized
+// words to a wave-private LDS scratch in the source-lane order of the prepared layout, applies
+// the patches (one per lane and tile; a wave whose lists exceed 64 entries in its split runs a
+// loop instance that continues from global memory) and reads the words back as B operands.
 //
 // DoRA H: DoRA blocks at the front of the grid compute, per 128-row activation block, shares
 // of X.A^T over strided 32-column steps; the last share of an activation block sums them in
 // share order, rounds H to fp16 and raises that block's ready slot.  The block that finishes
 // an output tile polls its slot before the epilogue (normally long raised by then).
 //
-// K splits (narrow layers, small M): fp32 partials in the accumulator register layout, summed
-// in split order by the last arrival of the tile.  Failures of the hand-offs set the
+// K splits only for layers longer than one split holds (> 191 slabs): fp32 partials in the
+// accumulator register layout, summed in split order by the last arrival of the tile.  Failures of the hand-offs set the
 // workspace's sticky error word and the rows concerned are written as fp16 NaN, as in the
 // decode kernel.
 //
