@@ -180,8 +180,10 @@ wlq::Dora make_dora(const void* lora_B, const float* lora_H, const void* dora_ga
 
 size_t round_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// lists: the layer's prepared patch lists (the GEMM reads its outliers from them), or nullptr
 int run_product(const wlq::Layer& L, wlq::Dora D, const void* X, void* out, int64_t M, void* workspace,
-                size_t workspace_bytes, hipStream_t stream, const char* fn) {
+                size_t workspace_bytes, hipStream_t stream, const char* fn,
+                const wlq::PatchLists* lists = nullptr) {
   if (M < 0 || M > 0x7fffffff / 4) {
     wlq::set_error("%s: bad M=%lld", fn, (long long)M);
     return WLQ_ERR_BAD_SHAPE;
@@ -231,8 +233,9 @@ int run_product(const wlq::Layer& L, wlq::Dora D, const void* X, void* out, int6
     }
     return hip_status(wlq::launch_skinny(L, D, x, y, (int)M, p, w, sync, stream), fn);
   }
-  const wlq::SplitPlan p = wlq::plan_gemm(L, (int)M, cus, ws);
-  return hip_status(wlq::launch_gemm(L, D, x, y, (int)M, p, w, stream), fn);
+  const bool use_lists = lists != nullptr && lists->nnz > 0 && L.offsets != nullptr;
+  const wlq::SplitPlan p = wlq::plan_gemm(L, (int)M, cus, ws, use_lists);
+  return hip_status(wlq::launch_gemm(L, D, x, y, (int)M, p, w, stream, use_lists ? lists : nullptr), fn);
 }
 
 // wlq_gemm_prepared with a workspace of the caller's (strict = false: a stream-kernel plan
@@ -254,13 +257,17 @@ int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c
   if (prepared != nullptr && M >= 1 && (M <= wlq::stream_max_m() || wide || prefill) && L.N > 0 && X != nullptr &&
       out != nullptr && wlq::prepared_supported(L.N, L.K, L.bits, L.group_size) && nnz >= 0 &&
       (L.offsets != nullptr || nnz == 0)) {
-    const size_t need = wlq::prepared_layout(L.N, L.K, L.group_size, nnz).bytes;
+    const wlq::PreparedLayout lay = wlq::prepared_layout(L.N, L.K, L.group_size, nnz);
+    const size_t need = lay.bytes;
     if (prepared_bytes < need) {
       wlq::set_error("%s: the prepared buffer holds %zu bytes, the layer needs %zu (nnz=%lld)", fn, prepared_bytes,
                      need, (long long)nnz);
       return WLQ_ERR_CAPACITY;
     }
     const bool fused_h = D.r > 0 && D.H == nullptr;
+    const char* pbase = reinterpret_cast<const char*>(prepared);
+    const wlq::PatchLists lists{reinterpret_cast<const uint32_t*>(pbase + lay.wpidx_off),
+                                reinterpret_cast<const uint32_t*>(pbase + lay.wpatch_off), nnz, lay.T, lay.S};
     // the kernel stages B rows with 16-byte loads (r % 8 == 0) and x / lora_A rows likewise
     const bool dora_ok = D.r == 0 || (D.r % 8 == 0 && D.r <= wlq::stream_max_rank() &&
                                       (reinterpret_cast<uintptr_t>(D.B) & 15u) == 0);
@@ -286,7 +293,7 @@ int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c
                                               reinterpret_cast<uint16_t*>(out), (int)M, p, w, sync, stream),
                           fn);
       }
-      return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, fn);
+      return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, fn, &lists);
     }
     if (wide) {
       const bool csr = L.offsets != nullptr && nnz > 0;
@@ -308,7 +315,7 @@ int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c
                                            reinterpret_cast<uint16_t*>(out), (int)M, p, w, sync, stream),
                           fn);
       }
-      return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, fn);
+      return run_product(L, D, X, out, M, workspace, workspace_bytes, stream, fn, &lists);
     }
     const wlq::StreamPlan p =
         wlq::plan_stream(L.N, L.K, (int)M, current_cu_count(), fused_h ? D.r : 0, L.chunk);

@@ -28,10 +28,17 @@
 //
 // The producer loop runs one 512-column outlier chunk (640 for 3-bit) per trip
 // with its steps unrolled, so everything tied to chunk boundaries is fixed at
-// compile time.  Outliers are prepared per (N tile, chunk) and producer thread by
-// tile_entries_kernel: a column mask per step and the values in column order; a W
-// thread holds its record in registers (loaded a chunk ahead) and writes the values
-// of a step's set bits over its dequantized columns.
+// compile time.  Outliers come from one of:
+// * the layer's prepared patch lists (a layer with a prepared buffer): per 16-row tile and
+//   128-column slab, the list of (row, column, e5m2) patches with duplicates resolved.  The
+//   32 threads of list l (the rows producer wave l / 2 dequantizes, so its LDS writes stay in
+//   program order behind that wave's tile stores) each take one entry per slab, loaded with
+//   the step's prefetch; the list starts of the block's K range sit in LDS.  A wave whose
+//   lists hold more than 32 entries in some slab walks its rows' CSR entries instead;
+// * records prepared per (N tile, chunk) and producer thread by tile_entries_kernel: a
+//   column mask per step and the values in column order, which a W thread writes over its
+//   dequantized columns;
+// * the row's CSR entries, walked directly (no workspace room for the records).
 //
 // DoRA: the low-rank term s * H . B^T is added in the epilogue of split 0 with
 // V_MFMA_F32_16X16X4_F32 (fp32 operands, exact products) and every split scales
@@ -64,6 +71,11 @@ constexpr int kOlVals = 8;
 constexpr int ol_slot_words(int spc) { return 3 * spc * NP; }
 constexpr int kMaxSplits = 32;
 constexpr int kXcds = 8;
+// Patch-list starts of a block's K range in LDS: 8 lists x (slabs + 1) words.  Prepared layers
+// have K <= 65535 (512 slabs; whole 640-column chunks reach 515).
+constexpr int kTabSlabs = 520;
+constexpr int kTabBytes = 8 * kTabSlabs * 4;
+enum OlMode : int { kOlDirect = 0, kOlRecords = 1, kOlLists = 2 };
 
 struct GemmArgs {
   const uint32_t* q;
@@ -85,6 +97,10 @@ struct GemmArgs {
   int tiles_m, tiles_n, tiles;
   int has_csr;
   const uint32_t* tent;  // outlier records [tiles_n * nch][ol_slot_words], or nullptr (direct CSR reads)
+  const uint32_t* wpidx;   // prepared patch lists (nullptr: records or CSR walk)
+  const uint32_t* wpatch;
+  uint32_t patch_bytes;
+  int T, S;                // prepared 16-row tiles and 128-column slabs
 };
 
 struct GemmSmem {
@@ -216,9 +232,11 @@ struct StepRegs {
   u32x4_t x[8];                             // activation units u = ptid + NP * j
   uint32_t cw[StepCodes<BITS>::kWords];     // code words of the thread's 32 columns
   LutRaw<BITS> lr;                          // group LUT of the step
+  uint32_t pe, pok;                         // patch-list entry of the step's slab, whether it is one
 };
 
-template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC>
+// LISTS: outliers from prepared patch lists (a.wpidx), otherwise records (a.tent) or the CSR walk.
+template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC, bool LISTS>
 __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   constexpr int NCB = 1 << BITS;
   constexpr int SPC = (BITS == 3 ? 640 : 512) / BK;  // K steps per outlier chunk (even)
@@ -249,8 +267,9 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   const int ck_end = (kt_end + SPC - 1) / SPC;
   const bool has_work = kt_begin < kt_end;
 
-  // Outlier records (when the workspace holds them) or direct reads of the CSR arrays.
-  const bool prepared = HAS_CSR && a.tent != nullptr;
+  // Outliers: prepared patch lists, records (when the workspace holds them) or direct reads of
+  // the CSR arrays.
+  const int ol_mode = !HAS_CSR ? kOlDirect : LISTS ? kOlLists : a.tent != nullptr ? kOlRecords : kOlDirect;
   const int prologue_barriers = 1;
 
   if (wave < 4) {
@@ -417,9 +436,34 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
     ov1 = vw[1];
   };
 
-  // Loads of step kt into S.  EVEN: the step's index from the range start is even.
-  auto load_step = [&](StepRegs<BITS>& S, int kt, auto even_c) __attribute__((always_inline)) {
+  // Patch lists: thread ptid takes entry ptid % 32 of list li = ptid / 32 of each slab, the list
+  // of prepared tile 8 tn + li (rows 16 li .. 16 li + 15 of the N tile, which producer wave li / 2
+  // dequantizes).  ltab[li][i]: start of the list of slab s_first + i; slabs past K hold empty
+  // lists.
+  const int li = ptid >> 5;
+  const int es = ptid & 31;
+  const int s_first = kt_begin >> 1;  // the range starts at a whole chunk (an even step)
+  const int ntab = (ck_end - ck_begin) * (SPC / 2) + 1;
+  uint32_t* ltab = reinterpret_cast<uint32_t*>(smem_raw + sizeof(GemmSmem));
+  const __amdgpu_buffer_rsrc_t rpatch = make_rsrc(a.wpatch, a.patch_bytes);
+
+  // Start and length of the list of step kt's slab (read a step before the loads that use them:
+  // right after a barrier the LDS queue holds the consumers' fragment reads).
+  auto list_of = [&](int kt, uint32_t& st, uint32_t& cnt) __attribute__((always_inline)) {
+    const int si = min((kt >> 1) - s_first, ntab - 2);
+    st = ltab[li * ntab + si];
+    cnt = ltab[li * ntab + si + 1] - st;
+  };
+  // Loads of step kt into S.  EVEN: the step's index from the range start is even.  LISTS: the
+  // thread's entry of list (st, cnt), the one of the step's slab.
+  auto load_step = [&](StepRegs<BITS>& S, int kt, auto even_c, auto lists_c, uint32_t st, uint32_t cnt)
+                       __attribute__((always_inline)) {
     constexpr bool kEven = decltype(even_c)::value;
+    if constexpr (decltype(lists_c)::value) {
+      const bool ok = (uint32_t)es < cnt;
+      S.pok = ok ? 1u : 0u;
+      S.pe = __builtin_amdgcn_raw_buffer_load_b32(rpatch, (int)(ok ? (st + (uint32_t)es) * 4u : kOutOfRange), 0, 0);
+    }
     const int k0 = kt * BK;
     if constexpr (X_VEC) {
       const bool in = k0 < xlim;
@@ -518,19 +562,75 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
     }
   };
 
+  // Patch of list entry pv over the W tile of step kt in buf (when it lies in the step's half of
+  // its slab): lane = row % 16 + 16 (column / 32) of the slab, bits 6..10 the column % 32.
+  auto apply_patch = [&](uint32_t pv, int kt, int buf) __attribute__((always_inline)) {
+    const uint32_t l6 = pv & 63u;
+    const uint32_t kq = l6 >> 4;
+    if ((int)(kq >> 1) == (kt & 1)) {
+      const uint32_t c32 = (pv >> 6) & 31u;
+      const int nlr = 16 * li + (int)(l6 & 15u);
+      sm.b[buf][nlr * BK + 8 * ((int)(4u * (kq & 1u) + (c32 >> 3)) ^ swz(nlr)) + (int)(c32 & 7u)] =
+          (uint16_t)((pv >> 24) << 8);
+    }
+  };
+  auto store_lists = [&](const StepRegs<BITS>& S, int kt, int buf) __attribute__((always_inline)) {
+    if (S.pok != 0u) apply_patch(S.pe, kt, buf);
+  };
+  // Wave w writes the list starts of lists 2w, 2w + 1 (the lists its threads read; LDS keeps a
+  // wave's accesses in order, so no barrier) and returns whether any of them is longer than 32
+  // entries in some slab of the range.
+  auto fill_lists = [&]() __attribute__((always_inline)) {
+    const int wv = ptid >> 6;
+    const int ln = ptid & 63;
+    for (int i0 = 0; i0 < 2 * ntab; i0 += 512) {
+      uint32_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + ln + 64 * j;
+        const int l = 2 * wv + (i >= ntab ? 1 : 0);
+        const int si = i >= ntab ? i - ntab : i;
+        const int ptl = 8 * tn + l;
+        v[j] = (i < 2 * ntab && ptl < a.T) ? a.wpidx[(size_t)ptl * a.S + min(s_first + si, a.S)] : 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + ln + 64 * j;
+        if (i < 2 * ntab) ltab[(2 * wv + (i >= ntab ? 1 : 0)) * ntab + (i >= ntab ? i - ntab : i)] = v[j];
+      }
+    }
+    bool lng = false;
+    for (int i = ln; i < 2 * ntab; i += 64) {
+      const int l = 2 * wv + (i >= ntab ? 1 : 0);
+      const int si = i >= ntab ? i - ntab : i;
+      if (si + 1 < ntab && ltab[l * ntab + si + 1] - ltab[l * ntab + si] > 32u) lng = true;
+    }
+    return __builtin_amdgcn_ballot_w64(lng) != 0;
+  };
+
   // Register sets: DIST steps of loads in flight (the sets rotate by step index; even
   // DIST keeps a set's step parity fixed, which the two-step group LUTs rely on).
   constexpr int DIST = (SPC % 4 == 0) ? 4 : 2;
-  auto run = [&](auto prep) __attribute__((always_inline)) {
-    constexpr bool kPrep = decltype(prep)::value;
+  auto run = [&](auto mode_c) __attribute__((always_inline)) {
+    constexpr int kMode = decltype(mode_c)::value;
+    constexpr bool kPrep = HAS_CSR && kMode == kOlRecords;
+    constexpr bool kLists = HAS_CSR && kMode == kOlLists;
+    const std::integral_constant<bool, kPrep> prep{};
+    const std::integral_constant<bool, kLists> lists{};
     StepRegs<BITS> rs[DIST];  // set d holds steps of index d (mod DIST) from the range start
-    if constexpr (HAS_CSR && kPrep) ol_issue(ck_begin, std::integral_constant<int, 0>{});
+    uint32_t pst = 0u, pcnt = 0u;  // list of the next step to load
+    if constexpr (kPrep) ol_issue(ck_begin, std::integral_constant<int, 0>{});
     static_for<0, DIST>([&](auto d_c) __attribute__((always_inline)) {
       constexpr int d = decltype(d_c)::value;
-      load_step(rs[d], kt_begin + d, std::integral_constant<bool, d % 2 == 0>{});
+      if constexpr (kLists) list_of(kt_begin + d, pst, pcnt);
+      load_step(rs[d], kt_begin + d, std::integral_constant<bool, d % 2 == 0>{}, lists, pst, pcnt);
     });
+    if constexpr (kLists) list_of(kt_begin + DIST, pst, pcnt);
     store_main(rs[0], kt_begin, 0, std::integral_constant<bool, true>{});
-    if constexpr (HAS_CSR) store_outliers(ck_begin, 0, std::integral_constant<int, 0>{}, prep);
+    if constexpr (kLists)
+      store_lists(rs[0], kt_begin, 0);
+    else if constexpr (HAS_CSR)
+      store_outliers(ck_begin, 0, std::integral_constant<int, 0>{}, prep);
     // drain the prologue's loads once: the loop then starts from the same wait state as
     // its back edge, and the compiler does not add first-iteration waits to every trip
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt/lgkmcnt unconstrained (gfx9 encoding)
@@ -545,14 +645,17 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
         constexpr int s = decltype(s_c)::value;
         constexpr int buf = s & 1;
         const int kt = kb + s;
-        if constexpr (HAS_CSR && kPrep)  // outlier record of the step staged below
+        if constexpr (kPrep)  // outlier record of the step staged below
           if (s + 1 < SPC || c + 1 < ck_end)
             ol_issue(s + 1 < SPC ? c : c + 1, std::integral_constant<int, (s + 1) % SPC>{});
-        load_step(rs[s % DIST], kt + DIST, std::integral_constant<bool, s % 2 == 0>{});
+        load_step(rs[s % DIST], kt + DIST, std::integral_constant<bool, s % 2 == 0>{}, lists, pst, pcnt);
         // keep the loads ahead of the stores of the other sets
         __builtin_amdgcn_sched_barrier(0);
         store_main(rs[(s + 1) % DIST], kt + 1, buf ^ 1, std::integral_constant<bool, (s + 1) % 2 == 0>{});
-        if constexpr (HAS_CSR) {
+        if constexpr (kLists) {
+          if (s + 1 < SPC || c + 1 < ck_end) store_lists(rs[(s + 1) % DIST], kt + 1, buf ^ 1);
+          list_of(kt + DIST + 1, pst, pcnt);  // done by the barrier's wait
+        } else if constexpr (HAS_CSR) {
           constexpr int KIN = ((s + 1) % SPC) * BK;
           if (s + 1 < SPC || c + 1 < ck_end)
             store_outliers(s + 1 < SPC ? c : c + 1, buf ^ 1, std::integral_constant<int, KIN>{}, prep);
@@ -561,10 +664,20 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
       });
     }
   };
-  if (prepared)
-    run(std::integral_constant<bool, true>{});
-  else
-    run(std::integral_constant<bool, false>{});
+  if constexpr (HAS_CSR && LISTS) {
+    // a wave with a list longer than its 32 threads in some slab walks its rows' CSR entries
+    if (fill_lists())
+      run(std::integral_constant<int, kOlDirect>{});
+    else
+      run(std::integral_constant<int, kOlLists>{});
+  } else if constexpr (HAS_CSR) {
+    if (ol_mode == kOlRecords)
+      run(std::integral_constant<int, kOlRecords>{});
+    else
+      run(std::integral_constant<int, kOlDirect>{});
+  } else {
+    run(std::integral_constant<int, kOlDirect>{});
+  }
 }
 
 // Outlier records: one block per (N tile, chunk), one thread per GEMM producer thread (row
@@ -621,9 +734,9 @@ __global__ __launch_bounds__(NP) void tile_entries_kernel(const int32_t* __restr
     if (s < spc) slot[s * NP + t] = mask[s];
 }
 
-template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC>
+template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC, bool LISTS = false>
 hipError_t launch_variant(const GemmArgs& a, dim3 grid, hipStream_t stream) {
-  auto* fn = gemm_kernel<BITS, LUTM, HAS_CSR, X_VEC>;
+  auto* fn = gemm_kernel<BITS, LUTM, HAS_CSR, X_VEC, LISTS>;
   // > 64 KiB of LDS is requested once per kernel and device
   static uint64_t attr_set = 0;
   int dev = 0;
@@ -632,16 +745,20 @@ hipError_t launch_variant(const GemmArgs& a, dim3 grid, hipStream_t stream) {
   const uint64_t bit = 1ull << (dev & 63);
   if (!(__atomic_load_n(&attr_set, __ATOMIC_ACQUIRE) & bit)) {
     e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)sizeof(GemmSmem));
+                            (int)(sizeof(GemmSmem) + kTabBytes));
     if (e != hipSuccess) return e;
     __atomic_fetch_or(&attr_set, bit, __ATOMIC_ACQ_REL);
   }
-  hipLaunchKernelGGL(fn, grid, dim3(NT), sizeof(GemmSmem), stream, a);
+  const size_t lds = sizeof(GemmSmem) + (a.wpidx != nullptr ? kTabBytes : 0);
+  hipLaunchKernelGGL(fn, grid, dim3(NT), lds, stream, a);
   return hipGetLastError();
 }
 
 template <int BITS, int LUTM, bool X_VEC>
 hipError_t launch_csr(const GemmArgs& a, dim3 grid, hipStream_t stream) {
+  if constexpr (X_VEC && (BITS == 4 || BITS == 3)) {  // prepared layers (3/4-bit) may bring patch lists
+    if (a.has_csr && a.wpidx != nullptr) return launch_variant<BITS, LUTM, true, true, true>(a, grid, stream);
+  }
   return a.has_csr ? launch_variant<BITS, LUTM, true, X_VEC>(a, grid, stream)
                    : launch_variant<BITS, LUTM, false, X_VEC>(a, grid, stream);
 }
@@ -670,15 +787,15 @@ hipError_t launch_any(const GemmArgs& a, int bits, int lutm, bool x_vec, dim3 gr
 
 }  // namespace
 
-SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes) {
+SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes, bool lists) {
   SplitPlan p{};
   const int ksteps = std::max(1, (L.K + BK - 1) / BK);
   const int spc = std::max(1, L.chunk / BK);
   const int nchunks = (ksteps + spc - 1) / spc;
   const long tiles = (long)((L.N + BN - 1) / BN) * (long)((M + BM - 1) / BM);
   const int target = std::max(1, cu_count);  // one 512-thread block per CU (LDS-bound)
-  // prepared outlier entries, when the workspace holds them
-  const size_t ent_bytes = (L.offsets != nullptr)
+  // per-call outlier records, when the workspace holds them (not with prepared patch lists)
+  const size_t ent_bytes = (L.offsets != nullptr && !lists)
                                ? (size_t)((L.N + BN - 1) / BN) * (size_t)L.nch * ol_slot_words(spc) * sizeof(uint32_t)
                                : 0;
   const size_t ent_room = workspace_bytes >= ent_bytes ? ent_bytes : 0;
@@ -701,7 +818,7 @@ SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes)
 }
 
 hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_t* out, int M,
-                       const SplitPlan& plan, float* workspace, hipStream_t stream) {
+                       const SplitPlan& plan, float* workspace, hipStream_t stream, const PatchLists* lists) {
   GemmArgs a{};
   a.q = L.q;
   a.lut = L.lut;
@@ -740,7 +857,23 @@ hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_
   if (L.group_size > 0 && L.ng > 1 && L.group_size % 32 != 0) return hipErrorInvalidValue;
   const size_t part_bytes = plan.splits > 1 ? (size_t)plan.splits * M * L.N * sizeof(float) : 0;
   a.tent = nullptr;
-  if (a.has_csr && plan.aux_bytes > 0) {
+  a.wpidx = nullptr;
+  a.wpatch = nullptr;
+  if (a.has_csr && lists != nullptr && lists->nnz > 0) {
+    // the list starts of a block's K range must fit the LDS table
+    const int spc = L.chunk / BK;
+    const int ksteps = (L.K + BK - 1) / BK;
+    const int nchunks = (ksteps + spc - 1) / spc;
+    const int cps = (plan.slabs_per_split + spc - 1) / spc;
+    if (lists->T != (L.N + 15) / 16 || lists->S != (L.K + 127) / 128 || (size_t)lists->nnz * 4 >= kOutOfRange ||
+        std::min(cps, nchunks) * (spc / 2) + 1 > kTabSlabs)
+      return hipErrorInvalidValue;
+    a.wpidx = lists->wpidx;
+    a.wpatch = lists->wpatch;
+    a.patch_bytes = (uint32_t)(lists->nnz * 4);
+    a.T = lists->T;
+    a.S = lists->S;
+  } else if (a.has_csr && plan.aux_bytes > 0) {
     a.tent = reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(workspace) + part_bytes);
     hipLaunchKernelGGL(tile_entries_kernel, dim3(a.tiles_n * L.nch), dim3(NP), 0, stream, L.offsets, L.cols,
                        L.vals, L.N, L.K, L.nch, L.chunk, const_cast<uint32_t*>(a.tent));

@@ -80,9 +80,19 @@ SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_byte
 hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint16_t* out, int M,
                          const SplitPlan& plan, float* workspace, uint32_t* sync, hipStream_t stream);
 
-SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes);
+// The outlier patch lists of a layer's prepared buffer (per 16-row tile and 128-column slab),
+// read by the GEMM in place of per-call outlier records.
+struct PatchLists {
+  const uint32_t* wpidx;    // [T * S + 1] list starts
+  const uint32_t* wpatch;   // [nnz] patches
+  int64_t nnz;
+  int T, S;
+};
+// lists: the GEMM takes the layer's outliers from prepared patch lists (no per-call records)
+SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes, bool lists = false);
 hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_t* out, int M,
-                       const SplitPlan& plan, float* workspace, hipStream_t stream);
+                       const SplitPlan& plan, float* workspace, hipStream_t stream,
+                       const PatchLists* lists = nullptr);
 
 hipError_t launch_dequant(const Layer& L, uint16_t* W, hipStream_t stream);
 
