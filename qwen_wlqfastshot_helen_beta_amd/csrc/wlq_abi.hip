@@ -216,7 +216,9 @@ int run_product(const wlq::Layer& L, wlq::Dora D, const void* X, void* out, int6
       return WLQ_ERR_CAPACITY;
     }
     float* H = reinterpret_cast<float*>(wbase);
-    int st = hip_status(wlq::launch_lora_h(x, D.A, (int)M, L.K, D.r, H, stream), fn);
+    // its K-chunk parts use the bytes after H (the product's part of the workspace, not yet in use)
+    float* part = ws > hb ? reinterpret_cast<float*>(wbase + hb) : nullptr;
+    int st = hip_status(wlq::launch_lora_h(x, D.A, (int)M, L.K, D.r, H, part, ws - hb, cus, stream), fn);
     if (st != WLQ_OK) return st;
     D.H = H;
     D.A = nullptr;
@@ -413,7 +415,8 @@ size_t wlq_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t bits, i
   const size_t hb = (r > 0 && !fused) ? round_up((size_t)M * r * sizeof(float)) : 0;
   const wlq::SplitPlan p = skinny ? wlq::plan_skinny(L, (int)M, cus, unlimited, fused ? r : 0)
                                   : wlq::plan_gemm(L, (int)M, cus, unlimited);
-  size_t need = hb + p.workspace_bytes;
+  const size_t hparts = hb > 0 ? wlq::lora_h_part_bytes((int)M, (int)K, r, cus) : 0;
+  size_t need = hb + std::max(p.workspace_bytes, hparts);
   if (M <= wlq::stream_max_m() && (bits == 4 || bits == 3)) {  // the prepared-layout kernel may serve the call
     const wlq::StreamPlan sp = wlq::plan_stream((int)N, (int)K, (int)M, cus,
                                                 r > 0 && r <= wlq::stream_max_rank() ? r : 0, L.chunk);

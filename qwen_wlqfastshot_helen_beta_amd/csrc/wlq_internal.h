@@ -165,7 +165,10 @@ hipError_t launch_finalize(const float* partial, int splits, int M, int N, const
                            int h_blocks, uint16_t* out, hipStream_t stream);
 
 // H[M, r] = fp32(fp16(X . A^T)) (the reference's F.linear in fp16, then .float()).
-hipError_t launch_lora_h(const uint16_t* X, const uint16_t* A, int M, int K, int r, float* H, hipStream_t stream);
+// H = fp32(fp16(X A^T)); part: room for K-chunk parts (lora_h_part_bytes), or null
+size_t lora_h_part_bytes(int M, int K, int r, int cu_count);
+hipError_t launch_lora_h(const uint16_t* X, const uint16_t* A, int M, int K, int r, float* H, float* part,
+                         size_t part_bytes, int cu_count, hipStream_t stream);
 
 // In-place epilogue on an fp16 output (the reference's separate pass).
 hipError_t launch_dora_epilogue(uint16_t* out, int M, int N, const Dora& D, hipStream_t stream);
