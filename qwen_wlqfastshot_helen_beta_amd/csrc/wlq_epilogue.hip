@@ -124,66 +124,17 @@ __device__ __forceinline__ u32x4_t load8z(const uint16_t* row, int k, int K, boo
   return v;
 }
 
-// H[M, r] = fp32(fp16(X . A^T)) for K <= 4096: one block per 16 x 16 tile of H, its 16 waves on K
-// slices of a multiple of 256 columns; each wave issues the 16 loads of 256 columns before their
-// 8 MFMAs (one load round trip).  Wave sums are added through LDS in wave order.
-constexpr int kH1Waves = 16;
-__global__ __launch_bounds__(1024) void lora_h_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ A,
-                                                      int M, int K, int r, float* __restrict__ H, int vec) {
-  __shared__ float red[kH1Waves][4][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int r16 = lane & 15;
-  const int kq = lane >> 4;
-  const int m0 = blockIdx.x * 16;
-  const int j0 = blockIdx.y * 16;
-  const int i = m0 + r16;
-  const int j = j0 + r16;
-  float4_t acc = {0.f, 0.f, 0.f, 0.f};
-  const uint16_t* xr = X + (size_t)min(i, M - 1) * K;
-  const uint16_t* ar = A + (size_t)min(j, r - 1) * K;
-  const int kslice = ((K + kH1Waves - 1) / kH1Waves + 255) / 256 * 256;
-  const int kb = wave * kslice;
-  const int ke = min(K, kb + kslice);
-  for (int k0 = kb; k0 < ke; k0 += 256) {
-    u32x4_t xa[8], ab[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int k = k0 + 32 * s + 8 * kq;
-      xa[s] = (i < M && k < ke) ? load8z(xr, k, ke, vec != 0) : u32x4_t{0u, 0u, 0u, 0u};
-      ab[s] = (j < r && k < ke) ? load8z(ar, k, ke, vec != 0) : u32x4_t{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) acc = mfma16x16x32(xa[s], ab[s], acc);
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) red[wave][e][lane] = acc[e];
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float v = 0.f;
-#pragma unroll
-      for (int w = 0; w < kH1Waves; ++w) v += red[w][e][lane];
-      const int ii = m0 + 4 * kq + e;
-      if (ii < M && j < r) H[(size_t)ii * r + j] = h2f(f2h_rn(v));
-    }
-  }
-}
-
-// H[M, r] = fp32(fp16(X . A^T)) for K > 4096, in K chunks: block (16-row tile of X, chunk ks,
-// 64-rank group z)
-// computes the 16 x 64 part of its chunk with MFMA 16x16x32 (both operands in natural k order); its 4 waves
-// take the chunk's 32-column steps in turn, 4 steps of loads in flight per wave, and their sums
-// meet in LDS in wave order.  One chunk: the block rounds and writes H; several: it writes its
-// fp32 part and lora_h_sum_kernel adds the parts in chunk order and rounds.
+// H[M, r] = fp32(fp16(X . A^T)) in K chunks: block (16-row tile of X, chunk ks, group z of 16 NT
+// ranks) computes the 16 x 16 NT part of its chunk with MFMA 16x16x32 (both operands in natural k
+// order); its 4 waves take the chunk's 32-column steps in turn, UNR steps of loads in flight per
+// wave, and their sums meet in LDS in wave order.  One chunk: the block rounds and writes H;
+// several: it writes its fp32 part and lora_h_sum_kernel adds the parts in chunk order and rounds.
 constexpr int kHWaves = 4;
-constexpr int kHTiles = 4;   // 16-rank tiles per block (64 ranks)
-constexpr int kHUnroll = 4;  // 32-column steps per wave and round
+template <int NT, int UNR>
 __global__ __launch_bounds__(64 * kHWaves) void lora_h_part_kernel(const uint16_t* __restrict__ X,
-                                                              const uint16_t* __restrict__ A, int M, int K, int r,
-                                                              int kch, float* __restrict__ out, int vec) {
-  __shared__ float red[kHWaves][kHTiles][4][64];
+                                                                   const uint16_t* __restrict__ A, int M, int K,
+                                                                   int r, int kch, float* __restrict__ out, int vec) {
+  __shared__ float red[kHWaves][NT][4][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r16 = lane & 15;
@@ -191,41 +142,41 @@ __global__ __launch_bounds__(64 * kHWaves) void lora_h_part_kernel(const uint16_
   const int m0 = blockIdx.x * 16;
   const int ks = blockIdx.y;
   const int i = m0 + r16;
-  const int j0 = 64 * blockIdx.z;
-  const int jt_n = min(kHTiles, (r - j0 + 15) >> 4);
+  const int j0 = 16 * NT * blockIdx.z;
+  const int jt_n = min(NT, (r - j0 + 15) >> 4);
   const int kb = ks * kch;
   const int ke = min(K, kb + kch);
-  float4_t acc[kHTiles];
+  float4_t acc[NT];
 #pragma unroll
-  for (int t = 0; t < kHTiles; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < NT; ++t) acc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
   const uint16_t* xr = X + (size_t)min(i, M - 1) * K;
-  for (int k0 = kb + 32 * wave; k0 < ke; k0 += 32 * kHWaves * kHUnroll) {
-    u32x4_t xa[kHUnroll], ab[kHUnroll][kHTiles];
+  for (int k0 = kb + 32 * wave; k0 < ke; k0 += 32 * kHWaves * UNR) {
+    u32x4_t xa[UNR], ab[UNR][NT];
 #pragma unroll
-    for (int u = 0; u < kHUnroll; ++u) {
+    for (int u = 0; u < UNR; ++u) {
       const int k = k0 + 32 * kHWaves * u + 8 * kq;
       const bool kin = k < ke;
       xa[u] = (i < M && kin) ? load8z(xr, k, ke, vec != 0) : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int t = 0; t < kHTiles; ++t) {
+      for (int t = 0; t < NT; ++t) {
         const int j = j0 + 16 * t + r16;
         ab[u][t] = (t < jt_n && j < r && kin) ? load8z(A + (size_t)j * K, k, ke, vec != 0) : u32x4_t{0u, 0u, 0u, 0u};
       }
     }
 #pragma unroll
-    for (int u = 0; u < kHUnroll; ++u)
+    for (int u = 0; u < UNR; ++u)
 #pragma unroll
-      for (int t = 0; t < kHTiles; ++t)
+      for (int t = 0; t < NT; ++t)
         if (t < jt_n) acc[t] = mfma16x16x32(xa[u], ab[u][t], acc[t]);
   }
 #pragma unroll
-  for (int t = 0; t < kHTiles; ++t)
+  for (int t = 0; t < NT; ++t)
 #pragma unroll
     for (int e = 0; e < 4; ++e) red[wave][t][e][lane] = acc[t][e];
   __syncthreads();
   const bool final_h = gridDim.y == 1;
   float* part = out + (size_t)ks * M * r;
-  for (int idx = threadIdx.x; idx < kHTiles * 256; idx += 64 * kHWaves) {
+  for (int idx = threadIdx.x; idx < NT * 256; idx += 64 * kHWaves) {
     const int t = idx >> 8;
     const int e = (idx >> 6) & 3;
     const int ln = idx & 63;
@@ -243,12 +194,20 @@ __global__ __launch_bounds__(64 * kHWaves) void lora_h_part_kernel(const uint16_
   }
 }
 
-// H[i] = fp32(fp16(sum of the chunk parts in chunk order)).
+// H[i] = fp32(fp16(sum of the chunk parts in chunk order)); the loads of 8 parts are issued
+// before their adds.
 __global__ __launch_bounds__(256) void lora_h_sum_kernel(const float* __restrict__ part, int chunks, size_t total,
                                                          float* __restrict__ H) {
   for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total; idx += (size_t)gridDim.x * 256) {
     float v = 0.f;
-    for (int c = 0; c < chunks; ++c) v += part[(size_t)c * total + idx];
+    for (int c0 = 0; c0 < chunks; c0 += 8) {
+      float t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = part[(size_t)min(c0 + u, chunks - 1) * total + idx];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (c0 + u < chunks) v += t[u];
+    }
     H[idx] = h2f(f2h_rn(v));
   }
 }
@@ -282,16 +241,16 @@ hipError_t launch_finalize(const float* partial, int splits, int M, int N, const
   return hipGetLastError();
 }
 
-// K chunks of lora_h_kernel: enough blocks for about four per CU, chunks of at least 512 columns.
+// K chunks of lora_h_part_kernel: enough blocks for about eight per CU, chunks of at least 512
+// columns.
 int lora_h_chunks(int M, int K, int cu_count) {
   const int tiles = std::max(1, (M + 15) / 16);
-  const int target = 4 * std::max(1, cu_count);
+  const int target = 8 * std::max(1, cu_count);
   const int most = std::max(1, (K + 511) / 512);
   return std::max(1, std::min(most, (target + tiles - 1) / tiles));
 }
 
 size_t lora_h_part_bytes(int M, int K, int r, int cu_count) {
-  if (K <= kH1Waves * 256) return 0;
   const int ks = lora_h_chunks(M, K, cu_count);
   return ks > 1 ? (size_t)ks * (size_t)M * (size_t)r * sizeof(float) : 0;
 }
@@ -301,19 +260,22 @@ hipError_t launch_lora_h(const uint16_t* X, const uint16_t* A, int M, int K, int
   if (M <= 0 || r <= 0) return hipSuccess;
   const int vec = ((reinterpret_cast<uintptr_t>(X) & 15u) == 0 && (reinterpret_cast<uintptr_t>(A) & 15u) == 0 &&
                    (K % 8) == 0) ? 1 : 0;
-  if (K <= kH1Waves * 256) {  // one load round trip per wave
-    const dim3 grid1((M + 15) / 16, (r + 15) / 16);
-    hipLaunchKernelGGL(lora_h_kernel, grid1, dim3(64 * kH1Waves), 0, stream, X, A, M, K, r, H, vec);
-    return hipGetLastError();
-  }
   int ks = lora_h_chunks(M, K, cu_count);
   const size_t per = (size_t)M * (size_t)r * sizeof(float);
   if (part == nullptr || (size_t)ks * per > part_bytes) ks = 1;  // no room for parts: one chunk
   const int kch = ks > 1 ? ((K + ks - 1) / ks + 31) / 32 * 32 : std::max(K, 1);
   ks = std::max(1, (K + kch - 1) / kch);
-  const dim3 grid((M + 15) / 16, ks, (r + 16 * kHTiles - 1) / (16 * kHTiles));
-  hipLaunchKernelGGL(lora_h_part_kernel, grid, dim3(64 * kHWaves), 0, stream, X, A, M, K, r, kch, ks > 1 ? part : H,
-                     vec);
+  float* dst = ks > 1 ? part : H;
+  if (r <= 16) {
+    hipLaunchKernelGGL((lora_h_part_kernel<1, 8>), dim3((M + 15) / 16, ks, 1), dim3(64 * kHWaves), 0, stream, X, A,
+                       M, K, r, kch, dst, vec);
+  } else if (r <= 32) {
+    hipLaunchKernelGGL((lora_h_part_kernel<2, 4>), dim3((M + 15) / 16, ks, 1), dim3(64 * kHWaves), 0, stream, X, A,
+                       M, K, r, kch, dst, vec);
+  } else {
+    hipLaunchKernelGGL((lora_h_part_kernel<4, 4>), dim3((M + 15) / 16, ks, (r + 63) / 64), dim3(64 * kHWaves), 0,
+                       stream, X, A, M, K, r, kch, dst, vec);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ks == 1) return e;
   const size_t total = (size_t)M * (size_t)r;
