@@ -43,7 +43,9 @@
 // DoRA: the low-rank term s * H . B^T is added in the epilogue of split 0 with
 // V_MFMA_F32_16X16X4_F32 (fp32 operands, exact products) and every split scales
 // by gamma; one split writes fp16((acc + s H B^T) * gamma), several write fp32
-// partials that splitk_sum_kernel adds and rounds.
+// partials that splitk_sum_kernel adds and rounds.  The producers stage the tile's H
+// rows, B rows and gamma in LDS (the K loop is over, every buffer is free; for r <= 16
+// the operands are loaded during the last K step), so the epilogue reads no global memory.
 //
 // Blocks are mapped so that each XCD works through a contiguous range of
 // tiles, N-tile major: consecutive blocks of one XCD share W tiles in its L2.
@@ -71,6 +73,14 @@ constexpr int kOlVals = 8;
 constexpr int ol_slot_words(int spc) { return 3 * spc * NP; }
 constexpr int kMaxSplits = 32;
 constexpr int kXcds = 8;
+// DoRA operands staged in LDS for the epilogue of split 0, kDr ranks per round (padded strides
+// against bank conflicts): fp32 H rows [BM][kDhStride], fp16 B rows [BN][kDbStride], gamma [BN].
+constexpr int kDr = 64;
+constexpr int kDrPre = 16;                    // ranks loaded during the last K step
+constexpr int kDhStride = kDr + 1;
+constexpr int kDbStride = kDr + 2;
+constexpr int kDbOff = BM * kDhStride * 4;    // bytes
+constexpr int kDgOff = kDbOff + BN * kDbStride * 2;
 // Patch-list starts of a block's K range in LDS: 8 lists x (slabs + 1) words.  Prepared layers
 // have K <= 65535 (512 slabs; whole 640-column chunks reach 515).
 constexpr int kTabSlabs = 520;
@@ -107,6 +117,7 @@ struct GemmSmem {
   uint16_t a[2][BM * BK];
   uint16_t b[2][BN * BK];
 };
+static_assert(kDgOff + BN * 2 <= (int)sizeof(GemmSmem), "staged DoRA operands fit the tile buffers");
 
 __device__ __forceinline__ int group_of(int col, uint32_t magic) { return (int)__umulhi((uint32_t)col, magic); }
 
@@ -329,44 +340,42 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
     // Epilogue.  Lane holds D[4*kq + e][r] of every 16x16 tile (i, j).  Split 0 adds the
     // DoRA term and every split scales by gamma (the split-K sum of gamma-scaled partials
     // is gamma times the sum), so the split-K reduce is a plain sum.
-    if (a.r > 0 && split == 0) {
+    const bool dora = a.r > 0 && split == 0;
+    if (dora) {
       // acc += s * H . B^T on the matrix core in fp32 (V_MFMA_F32_16X16X4_F32: A = s*H,
-      // lane l holds row l%16, k = l/16; B = B^T, lane l holds k = l/16, column l%16).
-      // 16 ranks per batch: all their H and B loads are issued before the batch's MFMAs, so a
-      // batch costs one load round trip (ranks past r read as zero).
-      for (int kb = 0; kb < a.r; kb += 16) {
-        float hv[4][8], bv[4][4];
+      // lane l holds row l%16, k = l/16; B = B^T, lane l holds k = l/16, column l%16), the
+      // operands read from the producers' staging (rows past M / N and ranks past r as zero).
+      const float* hb = reinterpret_cast<const float*>(smem_raw) + (128 * wm + r) * kDhStride + kq;
+      const uint16_t* bb = reinterpret_cast<const uint16_t*>(smem_raw + kDbOff) + (64 * wn + r) * kDbStride + kq;
+      for (int c0 = 0; c0 < a.r; c0 += kDr) {
+        __syncthreads();  // ranks c0 .. c0 + kDr - 1 staged
+        const int nr = min(kDr, a.r - c0);
+        for (int kb = 0; kb < nr; kb += 16) {
+          float hv[4][8], bv[4][4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int k = kb + 4 * u + kq;
-          const int kc = min(k, a.r - 1);
+          for (int u = 0; u < 4; ++u) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int ma = m0 + 128 * wm + 16 * i + r;
-            const float h = a.H[(size_t)min(ma, a.M - 1) * a.r + kc];
-            hv[u][i] = (ma < a.M && k < a.r) ? a.scale * h : 0.f;
+            for (int i = 0; i < 8; ++i) hv[u][i] = a.scale * hb[16 * i * kDhStride + kb + 4 * u];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bv[u][j] = h2f(bb[16 * j * kDbStride + kb + 4 * u]);
           }
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int n = n0 + 64 * wn + 16 * j + r;
-            const float b = h2f(a.B[(size_t)min(n, a.N - 1) * a.r + kc]);
-            bv[u][j] = (n < a.N && k < a.r) ? b : 0.f;
-          }
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[u][i], bv[u][j], acc[i][j], 0, 0, 0);
         }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(hv[u][i], bv[u][j], acc[i][j], 0, 0, 0);
+        if (c0 + kDr < a.r) __syncthreads();  // round read
       }
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = n0 + 64 * wn + 16 * j + r;
       if (n >= a.N) continue;
-      const float g = a.r > 0 ? h2f(a.gamma[n]) : 1.f;
+      const float g = dora ? h2f(reinterpret_cast<const uint16_t*>(smem_raw + kDgOff)[64 * wn + 16 * j + r])
+                           : a.r > 0 ? h2f(a.gamma[n]) : 1.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
 #pragma unroll
@@ -385,8 +394,31 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   }
 
   // -------------------------------------------------------------- producer waves
-  if (!has_work) return;
   const int ptid = tid - 4 * 64;
+
+  // DoRA operands of split 0: thread ptid stages H row m0 + ptid, half of B row n0 + ptid / 2
+  // and gamma of row n0 + ptid.  With r <= kDrPre they are loaded during the last K step.
+  const bool dora = a.r > 0 && split == 0;
+  const bool pre = dora && a.r <= kDrPre && has_work;
+  float dh[kDrPre];
+  uint16_t db[kDrPre / 2];
+  auto dora_pre = [&]() __attribute__((always_inline)) {
+    const int m = m0 + ptid;
+    const float* hrow = a.H + (size_t)min(m, a.M - 1) * a.r;
+#pragma unroll
+    for (int k = 0; k < kDrPre; ++k) {
+      const float v = hrow[min(k, a.r - 1)];
+      dh[k] = (m < a.M && k < a.r) ? v : 0.f;
+    }
+    const int nbr = n0 + (ptid >> 1);
+    const uint16_t* brow = a.B + (size_t)min(nbr, a.N - 1) * a.r;
+#pragma unroll
+    for (int k = 0; k < kDrPre / 2; ++k) {
+      const int rk = (kDrPre / 2) * (ptid & 1) + k;
+      const uint16_t v = brow[min(rk, a.r - 1)];
+      db[k] = (nbr < a.N && rk < a.r) ? v : (uint16_t)0;
+    }
+  };
 
   // A producer: units u = ptid + NP * j, row u / 8 = ptid / 8 + 32 j, columns 8 (ptid % 8) + [0, 8)
   // (eight lanes read one 128-byte row)
@@ -638,10 +670,11 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
 
     // One chunk per trip, its SPC steps unrolled.  Step s (the consumers run the MFMAs
     // of step kt meanwhile): loads of step kt+DIST, LDS stores of step kt+1 into the
-    // other buffer, barrier.
-    for (int c = ck_begin; c < ck_end; ++c) {
+    // other buffer, barrier.  The range's last step has no next step to stage; it loads the
+    // DoRA operands instead (r <= kDrPre).
+    auto chunk = [&](int c, auto nsteps_c) __attribute__((always_inline)) {
       const int kb = c * SPC;
-      static_for<0, SPC>([&](auto s_c) __attribute__((always_inline)) {
+      static_for<0, decltype(nsteps_c)::value>([&](auto s_c) __attribute__((always_inline)) {
         constexpr int s = decltype(s_c)::value;
         constexpr int buf = s & 1;
         const int kt = kb + s;
@@ -662,9 +695,15 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
         }
         __syncthreads();
       });
-    }
+    };
+    for (int c = ck_begin; c + 1 < ck_end; ++c) chunk(c, std::integral_constant<int, SPC>{});
+    chunk(ck_end - 1, std::integral_constant<int, SPC - 1>{});
+    if (pre) dora_pre();
+    __syncthreads();
   };
-  if constexpr (HAS_CSR && LISTS) {
+  if (!has_work) {
+    if (!dora) return;
+  } else if constexpr (HAS_CSR && LISTS) {
     // a wave with a list longer than its 32 threads in some slab walks its rows' CSR entries
     if (fill_lists())
       run(std::integral_constant<int, kOlDirect>{});
@@ -677,6 +716,49 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
       run(std::integral_constant<int, kOlDirect>{});
   } else {
     run(std::integral_constant<int, kOlDirect>{});
+  }
+  if (!dora) return;
+  // Staging, kDr ranks per round (the consumers read a round between two barriers).
+  float* hs = reinterpret_cast<float*>(smem_raw) + ptid * kDhStride;
+  uint16_t* bsr = reinterpret_cast<uint16_t*>(smem_raw + kDbOff) + (ptid >> 1) * kDbStride;
+  const int m = m0 + ptid;
+  const int nbr = n0 + (ptid >> 1);
+  for (int c0 = 0; c0 < a.r; c0 += kDr) {
+    if (c0 > 0) __syncthreads();  // the consumers read the previous round
+    const int nr = (min(kDr, a.r - c0) + 15) & ~15;  // ranks staged this round (zeros past r)
+    if (pre) {
+#pragma unroll
+      for (int k = 0; k < kDrPre; ++k) hs[k] = dh[k];
+#pragma unroll
+      for (int k = 0; k < kDrPre / 2; ++k) bsr[(kDrPre / 2) * (ptid & 1) + k] = db[k];
+    } else {
+      for (int k0 = 0; k0 < nr; k0 += 16) {
+        float hv[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const int rk = c0 + k0 + k;
+          const float v = a.H[(size_t)min(m, a.M - 1) * a.r + min(rk, a.r - 1)];
+          hv[k] = (m < a.M && rk < a.r) ? v : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) hs[k0 + k] = hv[k];
+      }
+      const int half = nr / 2;
+      for (int k0 = 0; k0 < half; k0 += 8) {
+        uint16_t bv[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int rk = c0 + half * (ptid & 1) + k0 + k;
+          const uint16_t v = a.B[(size_t)min(nbr, a.N - 1) * a.r + min(rk, a.r - 1)];
+          bv[k] = (nbr < a.N && rk < a.r) ? v : (uint16_t)0;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) bsr[half * (ptid & 1) + k0 + k] = bv[k];
+      }
+    }
+    if (c0 == 0 && ptid < BN)
+      reinterpret_cast<uint16_t*>(smem_raw + kDgOff)[ptid] = n0 + ptid < a.N ? a.gamma[n0 + ptid] : (uint16_t)0;
+    __syncthreads();  // round staged
   }
 }
 

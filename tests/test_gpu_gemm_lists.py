@@ -96,3 +96,16 @@ def test_gemm_lists_kernels(vw):
         pytest.skip("the profiler recorded no kernels of the library")
     assert any("gemm_kernel" in n for n in names), sorted(set(names))
     assert not any("tile_entries_kernel" in n for n in names), sorted(set(names))
+
+
+@pytest.mark.parametrize("rank", [8, 24, 48, 64, 80])
+def test_gemm_dora_ranks(vw, rank):
+    """The GEMM's DoRA epilogue reads H, B rows and gamma staged in LDS by the producer waves:
+    up to 16 ranks loaded during the last K step, more in rounds of 64 (80: two rounds, the
+    second partial), H computed by the library or given by the caller."""
+    for M, dora in ((200, "fused"), (300, "h")):
+        _case(M=M, rank=rank, dora=dora)
+        L = synth.make_layer(N=300, K=1408, bits=4, group_size=128, rank=rank, density=0.01, seed=rank + M)
+        x = synth.make_activations(M, L.K, seed=rank)
+        y, H = run_prepared(vw, L, x, dora=dora)
+        _check(y, L, x, H, f"rank={rank} M={M} dora={dora}")
