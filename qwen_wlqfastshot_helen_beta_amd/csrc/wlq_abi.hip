@@ -237,7 +237,7 @@ int run_product(const wlq::Layer& L, wlq::Dora D, const void* X, void* out, int6
   }
   const bool use_lists = lists != nullptr && lists->nnz > 0 && L.offsets != nullptr;
   const wlq::SplitPlan p = wlq::plan_gemm(L, (int)M, cus, ws, use_lists);
-  return hip_status(wlq::launch_gemm(L, D, x, y, (int)M, p, w, stream, use_lists ? lists : nullptr), fn);
+  return hip_status(wlq::launch_gemm(L, D, x, y, (int)M, p, w, stream, lists), fn);
 }
 
 // wlq_gemm_prepared with a workspace of the caller's (strict = false: a stream-kernel plan
@@ -268,8 +268,10 @@ int gemm_prepared_impl(const void* X, const int32_t* q_packed, const void* lut_c
     }
     const bool fused_h = D.r > 0 && D.H == nullptr;
     const char* pbase = reinterpret_cast<const char*>(prepared);
-    const wlq::PatchLists lists{reinterpret_cast<const uint32_t*>(pbase + lay.wpidx_off),
-                                reinterpret_cast<const uint32_t*>(pbase + lay.wpatch_off), nnz, lay.T, lay.S};
+    const wlq::PatchLists lists{reinterpret_cast<const uint32_t*>(pbase + lay.codes_off),
+                                reinterpret_cast<const uint32_t*>(pbase + lay.planes_off),
+                                reinterpret_cast<const uint32_t*>(pbase + lay.wpidx_off),
+                                reinterpret_cast<const uint32_t*>(pbase + lay.wpatch_off), nnz, lay.T, lay.S, lay.ng};
     // the kernel stages B rows with 16-byte loads (r % 8 == 0) and x / lora_A rows likewise
     const bool dora_ok = D.r == 0 || (D.r % 8 == 0 && D.r <= wlq::stream_max_rank() &&
                                       (reinterpret_cast<uintptr_t>(D.B) & 15u) == 0);

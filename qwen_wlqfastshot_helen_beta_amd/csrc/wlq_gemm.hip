@@ -111,6 +111,9 @@ struct GemmArgs {
   const uint32_t* wpatch;
   uint32_t patch_bytes;
   int T, S;                // prepared 16-row tiles and 128-column slabs
+  const uint32_t* pcodes;  // prepared codes and LUT planes (PREP kernels)
+  const uint32_t* pplanes;
+  int png;                 // LUT groups per row of the prepared planes
 };
 
 struct GemmSmem {
@@ -244,9 +247,13 @@ struct StepRegs {
   uint32_t cw[StepCodes<BITS>::kWords];     // code words of the thread's 32 columns
   LutRaw<BITS> lr;                          // group LUT of the step
   uint32_t pe, pok;                         // patch-list entry of the step's slab, whether it is one
+  u32x4_t plo, phi;                         // prepared LUT planes of the step's group (PREP)
 };
 
-// LISTS: outliers from prepared patch lists (a.wpidx), otherwise records (a.tent) or the CSR walk.
+// PREP: codes and LUT planes from the layer's prepared buffer (4-bit selector-ready nibbles; 3-bit
+// layers are stored there as nibbles with 16-entry planes), outliers from its patch lists; BITS then
+// only sets the outlier chunk (640 columns for 3-bit).  Otherwise the row-layout tensors, with
+// outlier records (a.tent) or the CSR walk.
 template <int BITS, int LUTM, bool HAS_CSR, bool X_VEC, bool LISTS>
 __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   constexpr int NCB = 1 << BITS;
@@ -444,8 +451,23 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
   const uint32_t qbase = (uint32_t)nbc * (uint32_t)a.wpr * 4u;
   const uint32_t lbase = (uint32_t)nbc * (uint32_t)(a.ng * NCB * 2);
 
+  // Prepared layout: this thread's 32 columns of step kt are the 16 bytes of lane
+  // (row % 16) + 16 (2 (kt % 2) + hh) of tile (n0 + nl) / 16, slab kt / 2; its row's LUT planes
+  // of group g are the 16-byte rows (row % 16) of planes [tile][g][0 / 1].
+  const int ptl = (n0 + nl) >> 4;
+  const __amdgpu_buffer_rsrc_t rpq = make_rsrc(a.pcodes, LISTS ? (uint32_t)((size_t)a.T * a.S * 1024) : 0u);
+  const __amdgpu_buffer_rsrc_t rpl = make_rsrc(a.pplanes, LISTS ? (uint32_t)((size_t)a.T * a.png * 512) : 0u);
+  const uint32_t pqbase = (uint32_t)((size_t)ptl * a.S * 1024 + (size_t)((nl & 15) + 16 * hh) * 16);
+  const uint32_t plbase = (uint32_t)((size_t)ptl * a.png * 512 + (size_t)(nl & 15) * 16);
+  LutPlanes<4> pp_row;
+  if constexpr (LISTS && LUTM == kLutRow) {
+    const u32x4_t lo = __builtin_amdgcn_raw_buffer_load_b128(rpl, (int)plbase, 0, 0);
+    const u32x4_t hi = __builtin_amdgcn_raw_buffer_load_b128(rpl, (int)(plbase + 256u), 0, 0);
+    pp_row.lo[0] = lo.x; pp_row.lo[1] = lo.y; pp_row.lo[2] = lo.z; pp_row.lo[3] = lo.w;
+    pp_row.hi[0] = hi.x; pp_row.hi[1] = hi.y; pp_row.hi[2] = hi.z; pp_row.hi[3] = hi.w;
+  }
   LutPlanes<BITS> pl_row;
-  if constexpr (LUTM == kLutRow) {
+  if constexpr (!LISTS && LUTM == kLutRow) {
     LutRaw<BITS> raw;
     lut_load_buf<BITS>(raw, rl, lbase, 0u);
     pl_row = lut_planes<BITS>(raw);
@@ -523,6 +545,17 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
       }
     }
     const int c0 = k0 + 32 * hh;
+    if constexpr (LISTS) {
+      const u32x4_t cv = __builtin_amdgcn_raw_buffer_load_b128(rpq, (int)(pqbase + (uint32_t)(kt >> 1) * 1024u +
+                                                                          (uint32_t)(kt & 1) * 512u), 0, 0);
+      S.cw[0] = cv.x; S.cw[1] = cv.y; S.cw[2] = cv.z; S.cw[3] = cv.w;
+      if constexpr (LUTM != kLutRow) {
+        const int g = min(group_of(c0, a.g_magic), a.png - 1);
+        S.plo = __builtin_amdgcn_raw_buffer_load_b128(rpl, (int)(plbase + (uint32_t)g * 512u), 0, 0);
+        S.phi = __builtin_amdgcn_raw_buffer_load_b128(rpl, (int)(plbase + (uint32_t)g * 512u + 256u), 0, 0);
+      }
+      return;
+    }
     load_codes<BITS>(rq, qbase, c0, S.cw);
     if constexpr (LUTM == kLutStep || (LUTM == kLutPair && kEven)) {
       const int g = min(group_of(k0, a.g_magic), a.ng - 1);  // uniform
@@ -538,6 +571,23 @@ __global__ __launch_bounds__(NT, 2) void gemm_kernel(const GemmArgs a) {
     constexpr bool kEven = decltype(even_c)::value;
 #pragma unroll
     for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4_t*>(&sm.a[buf][xoff + 32 * j * BK]) = S.x[j];
+    if constexpr (LISTS) {
+      LutPlanes<4> pp;
+      if constexpr (LUTM == kLutRow) {
+        pp = pp_row;
+      } else {
+        pp.lo[0] = S.plo.x; pp.lo[1] = S.plo.y; pp.lo[2] = S.plo.z; pp.lo[3] = S.plo.w;
+        pp.hi[0] = S.phi.x; pp.hi[1] = S.phi.y; pp.hi[2] = S.phi.z; pp.hi[3] = S.phi.w;
+      }
+      uint16_t* brow = &sm.b[buf][nl * BK];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        uint32_t o[4];
+        dequant_word4s(S.cw[u], pp, o);
+        *reinterpret_cast<u32x4_t*>(brow + 8 * ((4 * hh + u) ^ wsw)) = u32x4_t{o[0], o[1], o[2], o[3]};
+      }
+      return;
+    }
     LutPlanes<BITS> pl;
     if constexpr (LUTM == kLutRow) {
       pl = pl_row;
@@ -838,8 +888,11 @@ hipError_t launch_variant(const GemmArgs& a, dim3 grid, hipStream_t stream) {
 
 template <int BITS, int LUTM, bool X_VEC>
 hipError_t launch_csr(const GemmArgs& a, dim3 grid, hipStream_t stream) {
-  if constexpr (X_VEC && (BITS == 4 || BITS == 3)) {  // prepared layers (3/4-bit) may bring patch lists
-    if (a.has_csr && a.wpidx != nullptr) return launch_variant<BITS, LUTM, true, true, true>(a, grid, stream);
+  if constexpr (X_VEC && (BITS == 4 || BITS == 3)) {  // prepared layers (3/4-bit): codes, planes, patch lists
+    if (a.pcodes != nullptr) {
+      if (a.has_csr && a.wpidx != nullptr) return launch_variant<BITS, LUTM, true, true, true>(a, grid, stream);
+      if (!a.has_csr) return launch_variant<BITS, LUTM, false, true, true>(a, grid, stream);
+    }
   }
   return a.has_csr ? launch_variant<BITS, LUTM, true, X_VEC>(a, grid, stream)
                    : launch_variant<BITS, LUTM, false, X_VEC>(a, grid, stream);
@@ -941,6 +994,18 @@ hipError_t launch_gemm(const Layer& L, const Dora& D, const uint16_t* X, uint16_
   a.tent = nullptr;
   a.wpidx = nullptr;
   a.wpatch = nullptr;
+  a.pcodes = nullptr;
+  a.pplanes = nullptr;
+  if (lists != nullptr && (L.bits == 4 || L.bits == 3) && x_vec) {
+    if (lists->T != (L.N + 15) / 16 || lists->S != (L.K + 127) / 128 ||
+        (size_t)lists->T * lists->S * 1024 >= kOutOfRange || (size_t)lists->T * lists->ng * 512 >= kOutOfRange)
+      return hipErrorInvalidValue;
+    a.pcodes = lists->codes;
+    a.pplanes = lists->planes;
+    a.png = lists->ng;
+    a.T = lists->T;
+    a.S = lists->S;
+  }
   if (a.has_csr && lists != nullptr && lists->nnz > 0) {
     // the list starts of a block's K range must fit the LDS table
     const int spc = L.chunk / BK;

@@ -80,13 +80,16 @@ SplitPlan plan_skinny(const Layer& L, int M, int cu_count, size_t workspace_byte
 hipError_t launch_skinny(const Layer& L, const Dora& D, const uint16_t* x, uint16_t* out, int M,
                          const SplitPlan& plan, float* workspace, uint32_t* sync, hipStream_t stream);
 
-// The outlier patch lists of a layer's prepared buffer (per 16-row tile and 128-column slab),
-// read by the GEMM in place of per-call outlier records.
+// A layer's prepared buffer as the GEMM reads it: codes and LUT planes (per 16-row tile and
+// 128-column slab) in place of the row-layout tensors, and the outlier patch lists in place of
+// per-call outlier records.
 struct PatchLists {
+  const uint32_t* codes;    // u32x4 [T][S][64]
+  const uint32_t* planes;   // u32x4 [T][ng][2][16]
   const uint32_t* wpidx;    // [T * S + 1] list starts
   const uint32_t* wpatch;   // [nnz] patches
   int64_t nnz;
-  int T, S;
+  int T, S, ng;
 };
 // lists: the GEMM takes the layer's outliers from prepared patch lists (no per-call records)
 SplitPlan plan_gemm(const Layer& L, int M, int cu_count, size_t workspace_bytes, bool lists = false);

@@ -5,7 +5,7 @@ against the CPU oracle.  Cases: ragged N (N tiles of 128 rows with missing 16-ro
 (640-column chunks: five slabs per chunk), K splits (list starts of a block's range that do not
 begin at slab 0), dense outliers (lists longer than the 32 entries a list's threads take per
 slab: those waves walk their rows' CSR entries) and heavy rows (waves of both kinds in one
-block), DoRA H computed / given / off.  Tolerance: gpu_helpers.REL_TOL against the
+block), prepared layers without outliers, DoRA H computed / given / off.  Tolerance: gpu_helpers.REL_TOL against the
 single-rounding oracle and against the reference's fp16 rounding of x.W0^T
 (csrc/vllm_binding.cpp:355-393)."""
 from __future__ import annotations
@@ -109,3 +109,16 @@ def test_gemm_dora_ranks(vw, rank):
         x = synth.make_activations(M, L.K, seed=rank)
         y, H = run_prepared(vw, L, x, dora=dora)
         _check(y, L, x, H, f"rank={rank} M={M} dora={dora}")
+
+
+@pytest.mark.parametrize("bits", [4, 3])
+def test_gemm_prepared_codes_no_outliers(vw, bits):
+    """A prepared layer without outliers: the GEMM reads the prepared codes and LUT planes (3-bit
+    layers as nibbles with 16-entry planes) and applies no patches."""
+    for M, gs in ((150, 0), (300, 128), (260, 64)):
+        _case(M=M, gs=gs, bits=bits, csr=False)
+        L = synth.make_layer(N=330, K=1408 if bits == 4 else 1928, bits=bits, group_size=gs, rank=16, density=0.01,
+                             seed=bits * 100 + M + gs)
+        x = synth.make_activations(M, L.K, seed=M + gs)
+        y, H = run_prepared(vw, L, x, dora="fused", with_csr=False)
+        check_close(y, oracle_product(L, x, H, with_csr=False), what=f"no csr bits={bits} M={M} gs={gs}")
