@@ -872,11 +872,11 @@ PrefillPlan plan_prefill(int N, int K, int M, int group_size, int cu_count, int 
   p.workspace_bytes = hf + hp + part;
   p.lds = kLdsBytes;
   // Measured on MI355X (Qwen2.5-7B shapes, 4-bit, DoRA r = 16, 0.5% outliers): faster than the MFMA
-  // GEMM where the output tiles fill at least half the CUs without K splits and K is short
-  // (gate/up 18944 x 3584 at M = 256 / 512 / 1024: 82 / 160 / 242 us against 102 / 175 / 254;
-  // equal at M = 2048; q/o equal from M = 1024; slower on down 3584 x 18944 and below M = 1024 on
-  // narrow layers).
-  p.preferred = p.tiles >= cus / 2 && S <= 32 && M <= 1024;
+  // GEMM (256-row tiles) only where M leaves the GEMM's last row tile at most half full, on layers
+  // whose output tiles fill at least half the CUs without K splits (gate 18944 x 3584 at M = 384:
+  // 90 us against 144; at M = 256 / 512 / 768 / 1024 the GEMM's 77 / 146 / 151 / 220 us beat 83 /
+  // 162 / 168 / 246; slower on down 3584 x 18944 and on narrow layers).
+  p.preferred = p.tiles >= cus / 2 && S <= 32 && M <= 1024 && (M - 1) % 256 < 128;
   p.ok = sps <= kMaxSlabs && part < ((size_t)1 << 31) &&
          (splits == 1 || kSyncTile + p.mblk + p.tiles <= kSyncErrorWord) && kSyncTile + p.mblk <= kSyncErrorWord;
   return p;
