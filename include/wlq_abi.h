@@ -154,10 +154,10 @@ int wlq_prepare(const int32_t* q_packed, const void* lut_c, int64_t N, int64_t K
 /* wlq_gemm with the layer's prepared layout: M <= 8 runs the streaming decode
  * kernel on `prepared` (plus the reference chunk offsets) where its activation
  * staging fits, M = 9..128 the kernel that streams the activations through LDS
- * slab by slab, M = 129..1024 on wide layers the kernel that dequantizes W in
- * registers, every other case the MFMA GEMM on the reference-format codes and LUTs,
- * which stay required; all of these take their outliers from the prepared patch lists
- * (the GEMM of a row-layout call builds per-call outlier records instead).
+ * slab by slab, M = 129..1024 on wide layers with M mod 256 in 1..128 the kernel that
+ * dequantizes W in registers, every other case the MFMA GEMM; all of them read the
+ * prepared codes, LUT planes and outlier patch lists.  The reference-format tensors
+ * stay required (unaligned activations and other fallbacks run the row-layout kernels).
  * Replaces the same reference launchers as wlq_gemm / wlq_gemv
  * (csrc/vllm_binding.cpp:10-52, :318-419). */
 int wlq_gemm_prepared(const void* X, const int32_t* q_packed, const void* lut_c, const void* prepared,

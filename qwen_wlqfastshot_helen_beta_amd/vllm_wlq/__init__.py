@@ -6,8 +6,8 @@ fake implementations keep them traceable for graph capture and torch.compile --
 plus trailing defaulted arguments: ``group_size`` (0 = one LUT per row),
 ``lora_A`` (when lora_h / lora_H is None, the op computes the DoRA H itself as
 fp32(fp16(x @ lora_A^T)), the reference caller's F.linear) and ``prepared``
-(the layer's load-time tile-contiguous layout from ``_C.prepare_layer``, used by
-the product kernels up to 128 activation rows and, on wide layers, up to 1024).
+(the layer's load-time tile-contiguous layout from ``_C.prepare_layer``, which the
+product kernels read for every M: codes, LUT planes and outlier patch lists).
 Both call the ``_C`` extension, which calls the C ABI of ``libwlq_hip.so``.
 """
 from __future__ import annotations
